@@ -1,0 +1,162 @@
+"""Benchmark of the paged decode attention hot path on one MI355X.
+
+One step = one ragged paged decode attention over the whole batch
+(BASELINE config C2 by default: 64 sequences, contexts U[512, 8192] seeded,
+32 query / 8 KV heads, head_dim 128, bf16 pages of 16 tokens scattered over
+a pool 1.25x the pages used), inputs resident in HBM before timing.
+
+Prints ONE JSON line (the driver's contract) with:
+  value        tokens/s = sequences per step / wall time per step
+  roofline     the split kernel (dominant) timed with HIP events on its own
+               stream: algorithmic bytes per launch / its mean duration,
+               against MI355X's 8 TB/s HBM3E peak
+  cpu_baseline the PyTorch CPU restatement (page gather + masked GQA SDPA,
+               fp32) timed on a bounded sample of the same workload
+Extra decode configurations (--config c3 / c5) are available for study;
+the default line is C2.
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBPS = 8000.0   # MI355X HBM3E, AMD datasheet
+
+
+def algorithmic_bytes(case, kv_bytes_per_token_head):
+    """KV bytes read + Q read + O written + page-table entries read, one step."""
+    B, H, _, D = case['query'].shape
+    KH = case['cache_k'].shape[1]
+    ctx = sum(case['contexts'])
+    pages = sum(-(-c // 16) for c in case['contexts'])
+    q_o = 2 * B * H * D * case['query'].element_size()
+    return ctx * KH * kv_bytes_per_token_head + q_o + pages * 4
+
+
+def build_case(name, device):
+    from damendaemon_amd import workloads, kv_quant
+    if name == 'c2':
+        case = workloads.config_c2(device=device)
+        D = case['query'].shape[-1]
+        return case, 'C2 ragged paged decode bf16: 64 seqs, ctx U[512,8192] seed 2, H32/KH8/D128, page 16', \
+            'bf16', algorithmic_bytes(case, 2 * D * 2)
+    if name == 'c3':
+        case = workloads.config_c2(device=device)
+        D = case['query'].shape[-1]
+        case = workloads.quantize_pages(case, D, kv_quant)
+        return case, 'C3 ragged paged decode int8 KV (fp16 scale per token-head): C2 shapes', 'int8', \
+            algorithmic_bytes(case, 2 * (D + 2))
+    if name == 'c5':
+        case = workloads.config_c5(device=device)
+        D = case['query'].shape[-1]
+        return case, 'C5 long split-KV decode bf16: 16 x 32768, H16/KH2/D256, 1% K outliers x8', 'bf16', \
+            algorithmic_bytes(case, 2 * D * 2)
+    raise SystemExit(f'unknown config {name}')
+
+
+def cpu_baseline(case, budget_s=15.0, sample_seqs=16):
+    """Time oracle.decode_attention_sdpa (fp32, CPU) on the first sequences of the batch."""
+    from oracle import paged_oracle
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(threads)
+    n = min(sample_seqs, case['query'].shape[0])
+    table = case['page_table'][:n]
+    used = torch.unique(table[table >= 0]).long()
+    remap = torch.full((case['cache_k'].shape[0],), -1, dtype=torch.int64, device=used.device)
+    remap[used] = torch.arange(used.numel(), device=used.device)
+    small_table = torch.where(table >= 0, remap[table.clamp_min(0).long()], -1).to(torch.int32).cpu()
+    k = case['cache_k'][used].cpu()
+    v = case['cache_v'][used].cpu()
+    q = case['query'][:n].cpu()
+    pos = case['positions'][:n].cpu()
+    slots = torch.arange(n)
+    if k.dtype == torch.int8:
+        k = paged_oracle.dequantize_q8(k, case['k_scale'][used].cpu())
+        v = paged_oracle.dequantize_q8(v, case['v_scale'][used].cpu())
+    paged_oracle.decode_attention_sdpa(q, k, v, pos, slots, small_table)   # warm-up
+    times = []
+    start = time.perf_counter()
+    while len(times) < 10 or (time.perf_counter() - start < budget_s and len(times) < 200):
+        t0 = time.perf_counter()
+        paged_oracle.decode_attention_sdpa(q, k, v, pos, slots, small_table)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {'value': n / med, 'unit': 'tokens/s', 'cores': threads, 'kind': 'port',
+            'sample': f'first {n} of {case["query"].shape[0]} sequences (ctx sum '
+                      f'{sum(case["contexts"][:n])}), fp32 page gather + masked GQA SDPA, '
+                      f'median of {len(times)} runs'}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=50)
+    ap.add_argument('--warmup', type=int, default=5)
+    ap.add_argument('--config', default='c2', choices=['c2', 'c3', 'c5'])
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
+        print('bench.py measures one GPU only: this build has no multi-GPU path '
+              '(decode shards by sequence with no exchange; see the design notes)', file=sys.stderr)
+        raise SystemExit(2)
+
+    from damendaemon_amd import kernels
+    dev = 'cuda:0'
+    torch.cuda.set_device(0)
+    case, workload, dtype, nbytes = build_case(args.config, dev)
+    launch = kernels.prepare_attention(case['query'], case['cache_k'], case['cache_v'], case['positions'],
+                                       case['slots'], page_table=case['page_table'],
+                                       k_scale=case.get('k_scale'), v_scale=case.get('v_scale'))
+    for _ in range(args.warmup):
+        launch.run()
+    torch.cuda.synchronize()
+
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for e0, e1, e2 in events:
+        e0.record()
+        launch.partials()
+        e1.record()
+        launch.merge()
+        e2.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    split_ms = statistics.mean(e0.elapsed_time(e1) for e0, e1, _ in events)
+    merge_ms = statistics.mean(e1.elapsed_time(e2) for _, e1, e2 in events)
+    ms_per_step = wall / args.steps * 1e3
+    batch = case['query'].shape[0]
+    achieved = nbytes / (split_ms * 1e-3) / 1e9
+
+    line = {
+        'metric': 'paged decode attn tokens/s + achieved HBM GB/s (% peak), 1 MI355X',
+        'value': batch / (ms_per_step * 1e-3),
+        'unit': 'tokens/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': ms_per_step,
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': dtype,
+        'data': 'synthetic (seeded N(0,1) Q/K/V, seeded page scatter)',
+        'config': {'workload': workload, 'sequences': batch, 'context_tokens': sum(case['contexts']),
+                   'splits': launch.splits, 'split_tokens': launch.split_tokens,
+                   'split_kernel_ms': split_ms, 'merge_kernel_ms': merge_ms,
+                   'step_hbm_gbps': nbytes / (ms_per_step * 1e-3) / 1e9},
+        'roofline': {'bound': 'hbm', 'achieved': achieved, 'peak': PEAK_HBM_GBPS, 'unit': 'GB/s',
+                     'frac': achieved / PEAK_HBM_GBPS, 'traffic': None, 'algorithmic_bytes': nbytes},
+        'cpu_baseline': None if args.no_cpu_baseline else cpu_baseline(case),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == '__main__':
+    main()

@@ -1,0 +1,84 @@
+"""ctypes binding of the gfx950 shared library (the C ABI in include/).
+
+Mirrors the reference's native-library convention
+(damendaemon/native_q4.py:9-47): the library is opened once, its ABI
+version is checked, functions take plain device pointers, ints and a
+stream, and a non-zero return code becomes an exception here.
+
+There is no CPU fallback: every op in this package runs on the HIP
+kernels, and a missing or stale library raises instead of silently
+computing something else.
+"""
+import ctypes
+import os
+from functools import lru_cache
+from pathlib import Path
+
+import torch
+
+ABI_VERSION = 1
+LIBRARY = Path(__file__).resolve().parent / '_lib' / 'libdamendaemon_amd.so'
+
+F32, F16, BF16, I8 = 0, 1, 2, 3
+DTYPE_CODES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.int8: I8}
+
+_p, _i, _i64, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+
+# name -> argtypes (restype is always c_int)
+SIGNATURES = {
+    'dd_abi_version': [],
+    'dd_decode_splits': [_i, _i, ctypes.POINTER(_i)],
+    'dd_decode_attention': [_p, _i, _p, _p, _i, _p, _p, _i,   # q .. group
+                            _p, _p, _p, _i, _i,               # positions, slots, table, rows, width
+                            _i, _i, _i, _i, _i, _i64, _i, _f,  # B H KH D page cap window scale
+                            _p, _p, _i, _f, _p,               # alibi rel buckets denom sinks
+                            _p, _p, _p, _i, _i, _p],          # out part lse splits split_tokens stream
+}
+SIGNATURES['dd_quantize_q8'] = [_p, _i, _i64, _i, _i, _p, _p, _p]
+SIGNATURES['dd_dequantize_q8'] = [_p, _p, _i64, _i, _i, _p, _i, _p]
+SIGNATURES['dd_decode_partials'] = SIGNATURES['dd_decode_attention']
+SIGNATURES['dd_decode_merge'] = SIGNATURES['dd_decode_attention']
+
+
+class NativeError(RuntimeError):
+    pass
+
+
+@lru_cache(maxsize=1)
+def library():
+    path = os.environ.get('DAMENDAEMON_AMD_LIBRARY', str(LIBRARY))
+    if not Path(path).exists():
+        raise NativeError(f'{path} is missing: build it with '
+                          '`python -m damendaemon_amd.build` (no CPU fallback exists)')
+    handle = ctypes.CDLL(path)
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int
+    handle.dd_error_string.argtypes = [_i]
+    handle.dd_error_string.restype = ctypes.c_char_p
+    if handle.dd_abi_version() != ABI_VERSION:
+        raise NativeError('unsupported damendaemon_amd library ABI')
+    return handle
+
+
+def call(name, *args):
+    lib = library()
+    code = getattr(lib, name)(*args)
+    if code:
+        raise NativeError(f'{name} failed: {lib.dd_error_string(code).decode()} ({code})')
+
+
+def ptr(tensor):
+    return None if tensor is None else ctypes.c_void_p(tensor.data_ptr())
+
+
+def stream_of(tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(tensor.device).cuda_stream)
+
+
+def require_device(*tensors):
+    for t in tensors:
+        if t is not None and t.device.type != 'cuda':
+            raise ValueError('damendaemon_amd kernels need tensors on the GPU '
+                             '(there is no CPU path)')

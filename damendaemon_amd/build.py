@@ -1,0 +1,57 @@
+"""Compile the gfx950 HIP sources under csrc/ into one shared library.
+
+Objects are built in parallel with hipcc and linked into
+``damendaemon_amd/_lib/libdamendaemon_amd.so`` (in-tree, so the library
+travels with the source tree).  Every call recompiles: the build is the
+"does it build" check as well as the way to refresh the library.
+"""
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE / 'csrc'
+OUT_DIR = HERE / '_lib'
+LIBRARY = OUT_DIR / 'libdamendaemon_amd.so'
+ARCH = 'gfx950'
+HIPCC = os.environ.get('HIPCC', '/opt/rocm/bin/hipcc')
+FLAGS = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}',
+         # Packed FP32 instructions are kept out of every kernel.
+         '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+         '-Wno-unused-command-line-argument']
+
+
+def _compile(source, obj):
+    cmd = [HIPCC, *FLAGS, '-c', str(source), '-o', str(obj)]
+    run = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = '\n'.join(l for l in run.stderr.splitlines() if noise not in l)
+    if run.returncode:
+        raise RuntimeError(f'hipcc failed for {source.name}:\n{err}')
+    return err
+
+
+def build(jobs=None, verbose=False):
+    OUT_DIR.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob('*.hip'))
+    objs = [OUT_DIR / (s.stem + '.o') for s in sources]
+    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 4)), 16)
+    with ThreadPoolExecutor(jobs) as pool:
+        for warn in pool.map(_compile, sources, objs):
+            if warn and verbose:
+                print(warn, file=sys.stderr)
+    tmp = LIBRARY.with_suffix('.so.tmp')
+    link = [HIPCC, '-shared', f'--offload-arch={ARCH}', *map(str, objs), '-o', str(tmp)]
+    run = subprocess.run(link, capture_output=True, text=True)
+    if run.returncode:
+        raise RuntimeError('link failed:\n' + run.stderr)
+    os.replace(tmp, LIBRARY)
+    for o in objs:
+        o.unlink()
+    return LIBRARY
+
+
+if __name__ == '__main__':
+    print(build(verbose='-v' in sys.argv))

@@ -1,0 +1,117 @@
+// C entry points of the decode path.  The kernels are instantiated per
+// dtype pair in decode_<dtype>.hip so the library compiles in parallel.
+#include "decode_impl.h"
+
+using namespace dd_decode;
+
+extern template int dd_decode::dispatch_d<DD_BF16, DD_BF16>(const DecodeParams &, int, hipStream_t, int);
+extern template int dd_decode::dispatch_d<DD_F16, DD_F16>(const DecodeParams &, int, hipStream_t, int);
+extern template int dd_decode::dispatch_d<DD_F32, DD_F32>(const DecodeParams &, int, hipStream_t, int);
+extern template int dd_decode::dispatch_d<DD_I8, DD_BF16>(const DecodeParams &, int, hipStream_t, int);
+extern template int dd_decode::dispatch_d<DD_I8, DD_F16>(const DecodeParams &, int, hipStream_t, int);
+
+extern "C" int dd_decode_splits(int max_context, int batch_kv, int *split_tokens) {
+  if (max_context <= 0 || batch_kv <= 0) return -DD_EINVAL;
+  // Enough workgroups to cover 256 CUs several times over, but at least
+  // 256 keys per split so the per-split fixed cost stays small.
+  int st = 512;
+  while (st > 256 && (long)batch_kv * dd_cdiv(max_context, st) < 2048) st >>= 1;
+  while (st < 8192 && (long)batch_kv * dd_cdiv(max_context, st) > 16384) st <<= 1;
+  if (split_tokens) *split_tokens = st;
+  return (int)dd_cdiv(max_context, st);
+}
+
+static int decode_entry(int phase, const void *q, int q_dtype, const void *k, const void *v, int kv_dtype,
+                                   const void *k_scale, const void *v_scale, int group,
+                                   const int64_t *positions, const int64_t *slots, const int32_t *page_table,
+                                   int table_rows, int table_width, int batch, int heads, int kv_heads, int dim, int page_size,
+                                   int64_t capacity, int window, float scale, const float *alibi, const float *rel_bias,
+                                   int rel_buckets, float rel_denom, const float *sinks, void *out,
+                                   float *partial, float *lse, int splits, int split_tokens, void *stream) {
+  if (!q || !k || !v || !positions || !out || batch < 0 || capacity <= 0 || heads <= 0 || kv_heads <= 0 ||
+      heads % kv_heads || page_size <= 0 || splits <= 0 || split_tokens <= 0 || split_tokens % 64)
+    return DD_EINVAL;
+  if (batch == 0) return DD_OK;
+  if (splits > 1 && (!partial || !lse)) return DD_ESCRATCH;
+  DecodeParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.ks = (const unsigned short *)k_scale;
+  p.vs = (const unsigned short *)v_scale;
+  p.pos = positions;
+  p.slots = slots;
+  p.table = page_table;
+  p.out = out;
+  p.part = partial;
+  p.lse = lse;
+  p.alibi = alibi;
+  p.rel = rel_bias;
+  p.sinks = sinks;
+  p.B = batch;
+  p.H = heads;
+  p.KH = kv_heads;
+  p.G = heads / kv_heads;
+  p.table_w = table_width;
+  p.table_rows = table_rows;
+  p.page = page_size;
+  p.paged = page_table != nullptr;
+  p.window = window > 0 ? window : 0;
+  p.splits = splits;
+  p.split_tokens = split_tokens;
+  p.rel_buckets = rel_bias ? rel_buckets : 0;
+  p.rel_denom = rel_denom;
+  p.scale_log2 = scale * kLog2e;
+  p.group = group;
+  p.ngroups = group > 0 ? dim / group : 0;
+  if (p.paged) {
+    if (table_width <= 0 || page_size % 16) return DD_EUNSUPPORTED;
+    p.ctx_limit = table_width * page_size;
+  } else {
+    p.ctx_limit = page_size;
+  }
+  if ((long)p.ctx_limit > (long)splits * split_tokens) return DD_ESCRATCH;
+  p.capacity = capacity;
+  hipStream_t s = (hipStream_t)stream;
+  if (kv_dtype == DD_I8) {
+    if (!k_scale || !v_scale || group <= 0 || dim % group || (group % 32 && group != dim)) return DD_EINVAL;
+    if (q_dtype == DD_BF16) return dispatch_d<DD_I8, DD_BF16>(p, dim, s, phase);
+    if (q_dtype == DD_F16) return dispatch_d<DD_I8, DD_F16>(p, dim, s, phase);
+    return DD_EUNSUPPORTED;
+  }
+  if (q_dtype != kv_dtype) return DD_EINVAL;
+  if (kv_dtype == DD_BF16) return dispatch_d<DD_BF16, DD_BF16>(p, dim, s, phase);
+  if (kv_dtype == DD_F16) return dispatch_d<DD_F16, DD_F16>(p, dim, s, phase);
+  if (kv_dtype == DD_F32) return dispatch_d<DD_F32, DD_F32>(p, dim, s, phase);
+  return DD_EUNSUPPORTED;
+}
+
+extern "C" int dd_decode_attention(const void *q, int q_dtype, const void *k, const void *v, int kv_dtype,
+                                   const void *k_scale, const void *v_scale, int group,
+                                   const int64_t *positions, const int64_t *slots, const int32_t *page_table,
+                                   int table_rows, int table_width, int batch, int heads, int kv_heads, int dim, int page_size,
+                                   int64_t capacity, int window, float scale, const float *alibi, const float *rel_bias,
+                                   int rel_buckets, float rel_denom, const float *sinks, void *out,
+                                   float *partial, float *lse, int splits, int split_tokens, void *stream) {
+  return decode_entry(3, q, q_dtype, k, v, kv_dtype, k_scale, v_scale, group, positions, slots, page_table, table_rows, table_width, batch, heads, kv_heads, dim, page_size, capacity, window, scale, alibi, rel_bias, rel_buckets, rel_denom, sinks, out, partial, lse, splits, split_tokens, stream);
+}
+
+extern "C" int dd_decode_partials(const void *q, int q_dtype, const void *k, const void *v, int kv_dtype,
+                                   const void *k_scale, const void *v_scale, int group,
+                                   const int64_t *positions, const int64_t *slots, const int32_t *page_table,
+                                   int table_rows, int table_width, int batch, int heads, int kv_heads, int dim, int page_size,
+                                   int64_t capacity, int window, float scale, const float *alibi, const float *rel_bias,
+                                   int rel_buckets, float rel_denom, const float *sinks, void *out,
+                                   float *partial, float *lse, int splits, int split_tokens, void *stream) {
+  return decode_entry(1, q, q_dtype, k, v, kv_dtype, k_scale, v_scale, group, positions, slots, page_table, table_rows, table_width, batch, heads, kv_heads, dim, page_size, capacity, window, scale, alibi, rel_bias, rel_buckets, rel_denom, sinks, out, partial, lse, splits, split_tokens, stream);
+}
+
+extern "C" int dd_decode_merge(const void *q, int q_dtype, const void *k, const void *v, int kv_dtype,
+                                   const void *k_scale, const void *v_scale, int group,
+                                   const int64_t *positions, const int64_t *slots, const int32_t *page_table,
+                                   int table_rows, int table_width, int batch, int heads, int kv_heads, int dim, int page_size,
+                                   int64_t capacity, int window, float scale, const float *alibi, const float *rel_bias,
+                                   int rel_buckets, float rel_denom, const float *sinks, void *out,
+                                   float *partial, float *lse, int splits, int split_tokens, void *stream) {
+  return decode_entry(2, q, q_dtype, k, v, kv_dtype, k_scale, v_scale, group, positions, slots, page_table, table_rows, table_width, batch, heads, kv_heads, dim, page_size, capacity, window, scale, alibi, rel_bias, rel_buckets, rel_denom, sinks, out, partial, lse, splits, split_tokens, stream);
+}

@@ -1,0 +1,4 @@
+// Decode kernels instantiated for one KV dtype (see decode_impl.h).
+#include "decode_impl.h"
+
+template int dd_decode::dispatch_d<DD_F16, DD_F16>(const dd_decode::DecodeParams &, int, hipStream_t, int);

@@ -1,0 +1,580 @@
+// Ragged paged / slotted split-KV decode attention for gfx950.
+//
+// Replaces the reference's Triton `_attention` + `_merge` pair
+// (damendaemon/kernels.py:134-210) behind the same semantics:
+//   * one query row per sequence; keys 0..pos (optionally a trailing window),
+//     addressed through page_table[slot, t / page_size] (kernels.py:151-154)
+//     or a contiguous slot (kernels.py:155-157);
+//   * logits = q.k * scale (+ ALiBi slope * t, + T5 relative bias),
+//     fp32 softmax, fp32 accumulation; optional sink logits enlarge the
+//     denominator once (kernels.py:168-176, 198-206);
+//   * long contexts are split; splits are combined by log-sum-exp.
+//
+// MI355X design (not a translation of the Triton kernel):
+//   * one workgroup = one (sequence, KV head, split); its 4 wavefronts take
+//     interleaved 16-token pages, so every K/V byte is read once for the
+//     whole GQA group (the reference re-reads K/V per query head);
+//   * q.k for a 16-token page is a 16x16x32 MFMA (bf16/f16; int8 pages are
+//     widened exactly in registers), rows = the group's query heads,
+//     columns = the page's tokens;
+//   * p.v runs on the VALU from 16-byte coalesced loads, each lane owning a
+//     fixed 16-byte slice of the head dimension;
+//   * every wavefront keeps its own online softmax; the four are merged in
+//     LDS at the end of the split, and splits by a second small kernel.
+#pragma once
+#include "common.h"
+
+namespace dd_decode {
+
+struct DecodeParams {
+  const void *q;
+  const void *k;
+  const void *v;
+  const unsigned short *ks;
+  const unsigned short *vs;
+  const int64_t *pos;
+  const int64_t *slots;
+  const int32_t *table;
+  void *out;
+  float *part;
+  float *lse;
+  const float *alibi;
+  const float *rel;
+  const float *sinks;
+  long capacity;  // pages (paged) or slots (slotted); guards addressing
+  int B, H, KH, G;
+  int table_w, table_rows;
+  int page;       // page_size (paged) or context (slotted)
+  int ctx_limit;  // table_w * page (paged) or context (slotted)
+  int window;
+  int splits, split_tokens;
+  int group, ngroups;
+  int rel_buckets;
+  float rel_denom;
+  float scale_log2;
+  int paged;
+};
+
+constexpr int kWaves = 4;
+constexpr float kNegInf = -__builtin_inff();
+
+// Element offset of the first token of 16-token chunk `pg` of (row, kh), or
+// -1 when the chunk is not addressable (unallocated page-table entry).
+DD_DEV long chunk_base(const DecodeParams &p, int row, int kh, int pg, int D) {
+  if (p.paged) {
+    if (row < 0 || row >= p.table_rows) return -1;
+    const int tok = pg * 16;
+    const int entry = tok / p.page;
+    const long phys = p.table[(long)row * p.table_w + entry];
+    if (phys < 0 || phys >= p.capacity) return -1;
+    return ((phys * p.KH + kh) * (long)p.page + (tok % p.page)) * (long)D;
+  }
+  if (row < 0 || row >= p.capacity) return -1;
+  return (((long)row * p.KH + kh) * (long)p.page + (long)pg * 16) * (long)D;
+}
+
+// Convert 8 signed bytes to 8 exact bf16 / f16 MFMA operands.
+template <int QT>
+DD_DEV u32x4 widen_i8x8(u32x2 w) {
+  u32x4 r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const unsigned word = w[j >> 1];
+    const int a = (int)(signed char)(word >> (16 * (j & 1)));
+    const int b = (int)(signed char)(word >> (16 * (j & 1) + 8));
+    if constexpr (QT == DD_BF16) {
+      r[j] = (__float_as_uint((float)a) >> 16) | (__float_as_uint((float)b) & 0xffff0000u);
+    } else {
+      r[j] = (unsigned)float_to_f16_bits((float)a) | ((unsigned)float_to_f16_bits((float)b) << 16);
+    }
+  }
+  return r;
+}
+
+template <int QT>
+DD_DEV f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (QT == DD_BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+
+// Decode 16 bytes of V (one lane's slice of one token) into VE floats.
+template <int KVT, int VE>
+DD_DEV void widen_v(const u32x4 &w, float (&x)[VE]) {
+  if constexpr (KVT == DD_F32) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = __uint_as_float(w[e]);
+  } else if constexpr (KVT == DD_BF16) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = bf16_lo(w[e]);
+      x[2 * e + 1] = bf16_hi(w[e]);
+    }
+  } else if constexpr (KVT == DD_F16) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = f16_lo(w[e]);
+      x[2 * e + 1] = f16_hi(w[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) x[e] = (float)(int)(signed char)(w[e >> 2] >> (8 * (e & 3)));
+  }
+}
+
+// T5 relative-position bucket, restating kernels.py:162-167.
+DD_DEV int rel_bucket(int distance, int buckets, float denom) {
+  const int exact = buckets / 2;
+  if (distance < exact) return distance;
+  const int d = distance > exact ? distance : exact;
+  const int large = exact + (int)(logf((float)d / (float)exact) / denom * (float)(buckets - exact));
+  return large < buckets - 1 ? large : buckets - 1;
+}
+
+template <int KVT, int QT, int D, int GB>
+__global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
+  constexpr bool kMfma = KVT != DD_F32;
+  constexpr int VE = KVT == DD_F32 ? 4 : (KVT == DD_I8 ? 16 : 8);  // V elems per 16 B
+  constexpr int LPT = D / VE;                                       // lanes per V token
+  constexpr int TPI = 64 / LPT;                                     // tokens per V load
+  constexpr int NIT = (16 + TPI - 1) / TPI;                         // V loads per page
+  constexpr int NC = D / 32;                                        // MFMA k-chunks
+  constexpr int NC4 = D / 16;                                       // fp32 k-chunks
+  constexpr int KB = KVT == DD_F32 ? 4 : (KVT == DD_I8 ? 1 : 2);    // bytes per element
+
+  __shared__ float s_p[kWaves][16][GB];       // per-wave page probabilities
+  __shared__ float s_o[GB][D];                // cross-wave output accumulator
+  __shared__ float s_ml[kWaves][2][GB];       // per-wave running max / sum
+  __shared__ float s_q[kMfma ? 1 : GB][kMfma ? 1 : D];  // fp32 query (VALU q.k)
+
+  const int lane = threadIdx.x & 63;
+  const int w = uniform(threadIdx.x >> 6);
+  const int r = lane >> 4;
+  const int tl = lane & 15;
+  const int G = p.G;
+
+  const int wg = blockIdx.x;
+  const int split = wg % p.splits;
+  const int bkh = wg / p.splits;
+  const int b = bkh / p.KH;
+  const int kh = bkh % p.KH;
+
+  const long pos = p.pos[b];
+  const int row = p.slots ? (int)p.slots[b] : 0;
+  long t_hi = pos + 1;
+  if (t_hi > p.ctx_limit) t_hi = p.ctx_limit;
+  long t_lo = 0;
+  if (p.window > 0 && pos - p.window + 1 > 0) t_lo = pos - p.window + 1;
+  long s_lo = (long)split * p.split_tokens;
+  long s_hi = s_lo + p.split_tokens;
+  if (s_hi > t_hi) s_hi = t_hi;
+  if (s_lo < t_lo) s_lo = t_lo;
+  if (s_lo >= s_hi) return;  // empty split: the merge never reads it
+
+  const int pg_first = (int)(s_lo >> 4);
+  const int pg_last = (int)((s_hi - 1) >> 4);
+  const long head0 = (long)b * p.H + (long)kh * G;
+
+  // ---- query operand ----------------------------------------------------
+  u32x4 qa[kMfma ? NC : 1];
+  if constexpr (kMfma) {
+    const unsigned short *qb = (const unsigned short *)p.q;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      if (tl < G) {
+        qa[c] = *(const u32x4 *)(qb + (head0 + tl) * D + 8 * r + 32 * c);
+      } else {
+        qa[c] = u32x4{0, 0, 0, 0};
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < G * D; i += 256) {
+      s_q[i / D][i % D] = load_as<QT>(p.q, head0 * D + i);
+    }
+    __syncthreads();
+  }
+
+  // ---- per-wave online softmax state ------------------------------------
+  float m_run[GB];
+  float acc[GB][VE];
+  float lsum[4];
+#pragma unroll
+  for (int h = 0; h < GB; ++h) {
+    m_run[h] = kNegInf;
+#pragma unroll
+    for (int e = 0; e < VE; ++e) acc[h][e] = 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lsum[i] = 0.f;
+
+  const char *kbytes = (const char *)p.k;
+  const char *vbytes = (const char *)p.v;
+  const int vtok_lane = lane / LPT;        // token within a V load
+  const int vdim = VE * (lane % LPT);      // first dim of this lane's V slice
+  const bool v_lane_on = lane < LPT * TPI;
+
+  for (int pg = pg_first + w; pg <= pg_last; pg += kWaves) {
+    const long base = chunk_base(p, row, kh, pg, D);
+    const long t0 = (long)pg * 16;
+    const long tk = t0 + tl;
+    const bool kval = base >= 0 && tk >= s_lo && tk < s_hi;
+
+    // -- issue K and V loads for the page --
+    u32x4 kraw[kMfma ? NC : NC4];
+    u32x2 kraw8[KVT == DD_I8 ? NC : 1];
+    if constexpr (KVT == DD_I8) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        kraw8[c] = kval ? *(const u32x2 *)(kbytes + (base + (long)tl * D + 8 * r + 32 * c))
+                        : u32x2{0, 0};
+      }
+    } else if constexpr (kMfma) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        kraw[c] = kval ? *(const u32x4 *)(kbytes + 2 * (base + (long)tl * D + 8 * r + 32 * c))
+                       : u32x4{0, 0, 0, 0};
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < NC4; ++c) {
+        kraw[c] = kval ? *(const u32x4 *)(kbytes + 4 * (base + (long)tl * D + 4 * r + 16 * c))
+                       : u32x4{0, 0, 0, 0};
+      }
+    }
+    u32x4 vraw[NIT];
+    bool vval[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int tv = it * TPI + vtok_lane;
+      const long t = t0 + tv;
+      vval[it] = v_lane_on && tv < 16 && base >= 0 && t >= s_lo && t < s_hi;
+      vraw[it] = vval[it] ? *(const u32x4 *)(vbytes + KB * (base + (long)tv * D + vdim))
+                          : u32x4{0, 0, 0, 0};
+    }
+
+    // -- logits: lane holds token tl for heads 4r+i --
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (KVT == DD_I8) {
+      const unsigned short *ksc =
+          p.ks + (base / D + tl) * p.ngroups;  // scale row of this lane's token
+      if (p.group == D) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) s = mfma16x16x32<QT>(qa[c], widen_i8x8<QT>(kraw8[c]), s);
+        const float sc = kval ? half_bits_to_float(ksc[0]) : 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[i] *= sc;
+      } else {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const f32x4 part = mfma16x16x32<QT>(qa[c], widen_i8x8<QT>(kraw8[c]),
+                                              f32x4{0.f, 0.f, 0.f, 0.f});
+          const float sc = kval ? half_bits_to_float(ksc[(32 * c) / p.group]) : 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) s[i] += sc * part[i];
+        }
+      }
+    } else if constexpr (kMfma) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) s = mfma16x16x32<QT>(qa[c], kraw[c], s);
+    } else {
+      float part[GB];
+#pragma unroll
+      for (int h = 0; h < GB; ++h) part[h] = 0.f;
+#pragma unroll
+      for (int c = 0; c < NC4; ++c) {
+#pragma unroll
+        for (int h = 0; h < GB; ++h) {
+          const float *qrow = &s_q[h < G ? h : 0][4 * r + 16 * c];
+          part[h] += qrow[0] * __uint_as_float(kraw[c][0]) + qrow[1] * __uint_as_float(kraw[c][1]) +
+                     qrow[2] * __uint_as_float(kraw[c][2]) + qrow[3] * __uint_as_float(kraw[c][3]);
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < GB; ++h) {
+        part[h] += shfl(part[h], lane ^ 16);
+        part[h] += shfl(part[h], lane ^ 32);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float x = 0.f;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          if (4 * rr + i < GB && r == rr) x = part[4 * rr + i];
+        }
+        s[i] = x;
+      }
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int hg = 4 * r + i;  // head within the group
+      float x = s[i] * p.scale_log2;
+      if (p.alibi && hg < G) x += p.alibi[head0 - (long)b * p.H + hg] * kLog2e * (float)tk;
+      if (p.rel && hg < G) {
+        const long dist = pos - tk > 0 ? pos - tk : 0;
+        const int bucket = rel_bucket((int)dist, p.rel_buckets, p.rel_denom);
+        x += p.rel[(head0 - (long)b * p.H + hg) * p.rel_buckets + bucket] * kLog2e;
+      }
+      s[i] = kval ? x : kNegInf;
+    }
+
+    // -- page maxima per head, broadcast as wave-uniform values --
+    float rmax[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rmax[i] = row16_max(s[i]);
+    float m_use[GB], alpha[GB];
+    bool rescale = false;
+#pragma unroll
+    for (int h = 0; h < GB; ++h) {
+      const float mb = read_lane(rmax[h & 3], 16 * ((h >> 2) & 3));
+      const float mn = fmaxf(m_run[h], mb);
+      alpha[h] = mn == kNegInf ? 1.f : exp2f(m_run[h] - mn);
+      m_use[h] = mn == kNegInf ? 0.f : mn;
+      rescale |= alpha[h] != 1.f;
+      m_run[h] = mn;
+    }
+    if (rescale) {
+#pragma unroll
+      for (int h = 0; h < GB; ++h) {
+#pragma unroll
+        for (int e = 0; e < VE; ++e) acc[h][e] *= alpha[h];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float a = alpha[i < GB ? i : 0];
+#pragma unroll
+        for (int rr = 1; rr < 4; ++rr) {
+          if (4 * rr + i < GB && r == rr) a = alpha[4 * rr + i];
+        }
+        lsum[i] *= a;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float mm = m_use[i < GB ? i : 0];
+#pragma unroll
+      for (int rr = 1; rr < 4; ++rr) {
+        if (4 * rr + i < GB && r == rr) mm = m_use[4 * rr + i];
+      }
+      const float pr = exp2f(s[i] - mm);
+      lsum[i] += pr;
+      const int hg = 4 * r + i;
+      if (hg < G && hg < GB) s_p[w][tl][hg] = pr;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // -- p.v --
+    const unsigned short *vsc = nullptr;
+    if constexpr (KVT == DD_I8) vsc = p.vs + (base >= 0 ? base / D : 0) * p.ngroups + vdim / p.group;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      int tv = it * TPI + vtok_lane;
+      tv = tv < 16 ? tv : 15;
+      float pv[GB];
+#pragma unroll
+      for (int h = 0; h < GB; ++h) pv[h] = s_p[w][tv][h];
+      if constexpr (KVT == DD_I8) {
+        const float sc = vval[it] ? half_bits_to_float(vsc[(long)tv * p.ngroups]) : 0.f;
+#pragma unroll
+        for (int h = 0; h < GB; ++h) pv[h] *= sc;
+      }
+      float x[VE];
+      widen_v<KVT, VE>(vraw[it], x);
+#pragma unroll
+      for (int h = 0; h < GB; ++h) {
+#pragma unroll
+        for (int e = 0; e < VE; ++e) acc[h][e] += pv[h] * x[e];
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  // ---- reduce inside the wave ---------------------------------------------
+  float lw[GB];
+  {
+    float rs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rs[i] = row16_sum(lsum[i]);
+#pragma unroll
+    for (int h = 0; h < GB; ++h) lw[h] = read_lane(rs[h & 3], 16 * ((h >> 2) & 3));
+  }
+  if constexpr ((TPI & (TPI - 1)) == 0 && (LPT & (LPT - 1)) == 0) {
+#pragma unroll
+    for (int off = LPT; off < LPT * TPI; off <<= 1) {
+#pragma unroll
+      for (int h = 0; h < GB; ++h) {
+#pragma unroll
+        for (int e = 0; e < VE; ++e) acc[h][e] += shfl(acc[h][e], lane ^ off);
+      }
+    }
+  } else {
+    float tot[GB][VE];
+#pragma unroll
+    for (int h = 0; h < GB; ++h) {
+#pragma unroll
+      for (int e = 0; e < VE; ++e) tot[h][e] = acc[h][e];
+    }
+#pragma unroll
+    for (int g = 1; g < TPI; ++g) {
+      const int src = (lane + g * LPT) & 63;
+#pragma unroll
+      for (int h = 0; h < GB; ++h) {
+#pragma unroll
+        for (int e = 0; e < VE; ++e) tot[h][e] += shfl(acc[h][e], src);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < GB; ++h) {
+#pragma unroll
+      for (int e = 0; e < VE; ++e) acc[h][e] = tot[h][e];
+    }
+  }
+
+  // ---- merge the four wavefronts in LDS ------------------------------------
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < GB; ++h) {
+      s_ml[w][0][h] = m_run[h];
+      s_ml[w][1][h] = lw[h];
+    }
+  }
+  __syncthreads();
+  float mtot[GB], fac[GB];
+#pragma unroll
+  for (int h = 0; h < GB; ++h) {
+    float mm = s_ml[0][0][h];
+#pragma unroll
+    for (int ww = 1; ww < kWaves; ++ww) mm = fmaxf(mm, s_ml[ww][0][h]);
+    mtot[h] = mm;
+    fac[h] = m_run[h] == kNegInf ? 0.f : exp2f(m_run[h] - mm);
+  }
+#pragma unroll
+  for (int ww = 0; ww < kWaves; ++ww) {
+    if (w == ww && lane < LPT) {
+#pragma unroll
+      for (int h = 0; h < GB; ++h) {
+        if (h < G) {
+#pragma unroll
+          for (int e = 0; e < VE; ++e) {
+            const float val = acc[h][e] * fac[h];
+            s_o[h][vdim + e] = ww == 0 ? val : s_o[h][vdim + e] + val;
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  for (int i = threadIdx.x; i < G * D; i += 256) {
+    const int h = i / D;
+    const int d = i % D;
+    float mm = s_ml[0][0][h];
+    for (int ww = 1; ww < kWaves; ++ww) mm = fmaxf(mm, s_ml[ww][0][h]);
+    float l = 0.f;
+    for (int ww = 0; ww < kWaves; ++ww) {
+      const float mw = s_ml[ww][0][h];
+      if (mw != kNegInf) l += s_ml[ww][1][h] * exp2f(mw - mm);
+    }
+    float o = s_o[h][d];
+    const long bh = head0 + h;
+    if (p.splits == 1) {
+      if (p.sinks) {
+        const float sk = p.sinks[bh - (long)b * p.H] * kLog2e;
+        const float m2 = fmaxf(mm, sk);
+        const float f = exp2f(mm - m2);
+        l = l * f + exp2f(sk - m2);
+        o *= f;
+      }
+      store_as<QT>(p.out, bh * D + d, o / l);
+    } else {
+      p.part[(bh * p.splits + split) * D + d] = o / l;
+      if (d == 0) p.lse[bh * p.splits + split] = mm + log2f(l);
+    }
+  }
+  (void)mtot;
+}
+
+// Log-sum-exp combine of the split partials (restates kernels.py:191-210,
+// in base-2).  One workgroup per (sequence, head); only the splits that
+// overlap the sequence's live keys are read.
+template <int QT>
+__global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int D) {
+  const long bh = blockIdx.x;
+  const int b = (int)(bh / p.H);
+  const int h = (int)(bh % p.H);
+  const long pos = p.pos[b];
+  long t_hi = pos + 1;
+  if (t_hi > p.ctx_limit) t_hi = p.ctx_limit;
+  long t_lo = 0;
+  if (p.window > 0 && pos - p.window + 1 > 0) t_lo = pos - p.window + 1;
+  const int s0 = (int)(t_lo / p.split_tokens);
+  const int s1 = t_hi > t_lo ? (int)((t_hi - 1) / p.split_tokens) : s0 - 1;
+  const float *lse = p.lse + bh * p.splits;
+  float mm = -__builtin_inff();
+  for (int s = s0; s <= s1; ++s) mm = fmaxf(mm, lse[s]);
+  float sk = 0.f;
+  if (p.sinks) {
+    sk = p.sinks[h] * kLog2e;
+    mm = fmaxf(mm, sk);
+  }
+  float den = 0.f;
+  for (int s = s0; s <= s1; ++s) den += exp2f(lse[s] - mm);
+  if (p.sinks) den += exp2f(sk - mm);
+  const float inv = 1.f / den;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float o = 0.f;
+    for (int s = s0; s <= s1; ++s) o += exp2f(lse[s] - mm) * inv * p.part[(bh * p.splits + s) * D + d];
+    store_as<QT>(p.out, bh * D + d, o);
+  }
+}
+
+// phase bit 1: split kernel; bit 2: merge kernel (only when splits > 1).
+template <int KVT, int QT, int D, int GB>
+int launch_decode(const DecodeParams &p, hipStream_t stream, int phase) {
+  const long grid = (long)p.B * p.KH * p.splits;
+  if (grid <= 0) return DD_OK;
+  if (grid > 0x7fffffffL) return DD_EINVAL;
+  if (phase & 1) {
+    hipLaunchKernelGGL((decode_kernel<KVT, QT, D, GB>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    DD_LAUNCH_CHECK();
+  }
+  if ((phase & 2) && p.splits > 1) {
+    hipLaunchKernelGGL((merge_kernel<QT>), dim3((unsigned)((long)p.B * p.H)), dim3(D < 256 ? D : 256), 0,
+                       stream, p, D);
+    DD_LAUNCH_CHECK();
+  }
+  return DD_OK;
+}
+
+template <int KVT, int QT, int D>
+int dispatch_g(const DecodeParams &p, hipStream_t s, int phase) {
+  if (p.G <= 1) return launch_decode<KVT, QT, D, 1>(p, s, phase);
+  if (p.G <= 2) return launch_decode<KVT, QT, D, 2>(p, s, phase);
+  if (p.G <= 4) return launch_decode<KVT, QT, D, 4>(p, s, phase);
+  if (p.G <= 8) return launch_decode<KVT, QT, D, 8>(p, s, phase);
+  if (p.G <= 16) return launch_decode<KVT, QT, D, 16>(p, s, phase);
+  return DD_EUNSUPPORTED;
+}
+
+// Instantiated once per dtype pair in decode_<dtype>.hip.
+template <int KVT, int QT>
+int dispatch_d(const DecodeParams &p, int D, hipStream_t s, int phase) {
+  switch (D) {
+    case 64: return dispatch_g<KVT, QT, 64>(p, s, phase);
+    case 96: return dispatch_g<KVT, QT, 96>(p, s, phase);
+    case 128: return dispatch_g<KVT, QT, 128>(p, s, phase);
+    case 256: return dispatch_g<KVT, QT, 256>(p, s, phase);
+    default: return DD_EUNSUPPORTED;
+  }
+}
+
+}  // namespace dd_decode
+

@@ -1,0 +1,95 @@
+"""Q8_0 KV codec on the GPU, with the reference API of damendaemon/kv_quant.py.
+
+``quantize_kv``/``dequantize_kv`` keep the reference signatures and the
+reference format by default (one fp16 scale per gcd(dim, 32) channels,
+kv_quant.py:23-31); the ``group`` keyword extends them to any channel group
+that divides the head (``group=dim`` is one scale per (token, KV head)).
+Arithmetic is bit-identical to the reference (see csrc/quant.hip).
+"""
+import math
+
+import torch
+
+from . import _native
+from ._native import DTYPE_CODES, call, ptr, stream_of
+
+GROUP = 32
+
+
+def group_for(dim):
+    """Channel group of the reference format: gcd(dim, 32)."""
+    return math.gcd(int(dim), GROUP)
+
+
+def allocate_kv(max_batch, kv_heads, context, dim, device, group=None):
+    """(data, scales) of one layer: (2, batch, KH, context, dim) int8 and
+    (2, batch, KH, context, dim/group) fp16, zero-filled (kv_quant.py:34-45)."""
+    group = group or group_for(dim)
+    if dim % group or context <= 0 or max_batch <= 0 or kv_heads <= 0:
+        raise ValueError('invalid quantized KV geometry')
+    data = torch.zeros((2, max_batch, kv_heads, context, dim), dtype=torch.int8, device=device)
+    scales = torch.zeros((2, max_batch, kv_heads, context, dim // group), dtype=torch.float16, device=device)
+    return data, scales
+
+
+def quantize_kv(values, group=None):
+    """int8 values and fp16 scales (..., dim/group) of ``values`` (..., tokens, dim)."""
+    dim = values.shape[-1]
+    group = group or group_for(dim)
+    if values.ndim < 2 or dim % group:
+        raise ValueError('quantized KV requires a valid channel-group geometry')
+    _native.require_device(values)
+    if values.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise ValueError('quantized KV input must be fp32, fp16 or bf16')
+    x = values.contiguous()
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    s = torch.empty((*x.shape[:-1], dim // group), dtype=torch.float16, device=x.device)
+    call('dd_quantize_q8', ptr(x), DTYPE_CODES[x.dtype], x.numel() // dim, dim, group, ptr(q), ptr(s),
+         stream_of(x))
+    return q, s
+
+
+def dequantize_kv(data, scales, dtype):
+    """int8 * float(scale), rounded once to ``dtype`` (kv_quant.py:67-76)."""
+    if data.dtype != torch.int8 or scales.dtype != torch.float16:
+        raise ValueError('quantized KV requires int8 values with FP16 scales')
+    dim = data.shape[-1]
+    if scales.shape[:-1] != data.shape[:-1] or dim % scales.shape[-1]:
+        raise ValueError('incompatible quantized KV shapes')
+    _native.require_device(data, scales)
+    group = dim // scales.shape[-1]
+    d, s = data.contiguous(), scales.contiguous()
+    out = torch.empty(d.shape, dtype=dtype, device=d.device)
+    call('dd_dequantize_q8', ptr(d), ptr(s), d.numel() // dim, dim, group, ptr(out), DTYPE_CODES[dtype],
+         stream_of(d))
+    return out
+
+
+def store_kv(cache, slots, positions, k, v):
+    """Quantise K/V (batch, KH, tokens, dim) into (slot, position) rows of the
+    dense resident pair (kv_quant.py:79-107)."""
+    data, scales = cache
+    if positions.ndim != 2 or positions.shape[0] != k.shape[0] or positions.shape[1] != k.shape[2]:
+        raise ValueError('quantized KV store requires (batch, tokens) positions')
+    group = data.shape[-1] // scales.shape[-1]
+    if k.ndim != 4 or v.shape != k.shape or k.shape[0] != len(slots) or k.shape[-1] % group:
+        raise ValueError('quantized KV store requires matching batch-major K/V')
+    if positions.numel() and int(positions.max()) >= data.shape[3]:
+        raise ValueError('KV store position exceeds the cache context')
+    packed_k, scale_k = quantize_kv(k, group)
+    packed_v, scale_v = quantize_kv(v, group)
+    for row in range(k.shape[0]):
+        slot = int(slots[row])
+        p = positions[row]
+        data[0, slot][:, p, :] = packed_k[row]
+        data[1, slot][:, p, :] = packed_v[row]
+        scales[0, slot][:, p, :] = scale_k[row]
+        scales[1, slot][:, p, :] = scale_v[row]
+
+
+def read_kv(cache, slots, end, dtype=torch.float32):
+    """Dequantised (slots, KH, end, dim) K and V of the populated prefix (kv_quant.py:110-122)."""
+    data, scales = cache
+    d = data.index_select(1, slots)[..., :end, :]
+    s = scales.index_select(1, slots)[..., :end, :]
+    return dequantize_kv(d[0], s[0], dtype), dequantize_kv(d[1], s[1], dtype)

@@ -1,0 +1,144 @@
+/*
+ * damendaemon_amd — C ABI of the MI355X (gfx950) paged-attention hot path.
+ *
+ * Conventions (mirroring the reference's ctypes-loaded native libraries,
+ * damendaemon/native_q4.py:9-47):
+ *   - every entry point returns int: 0 on success, a DD_E* code otherwise;
+ *     dd_error_string() names the code;
+ *   - buffers are plain device pointers owned by the caller (PyTorch);
+ *     the library never allocates device memory;
+ *   - `stream` is a hipStream_t passed as void* (NULL = legacy default);
+ *     every launch is asynchronous on that stream and no entry point
+ *     synchronises, so all of them can be recorded into a HIP graph;
+ *   - dtype codes are DD_F32 / DD_F16 / DD_BF16 / DD_I8.
+ *
+ * KV page layout (damendaemon/paged.py:31-34): one layer's cache is
+ * (2, capacity, kv_heads, page_size, dim); K and V are the two planes.
+ * A slotted (non-paged) cache is (slots, kv_heads, context, dim)
+ * (damendaemon/kernels.py:152-154).
+ */
+#ifndef DAMENDAEMON_AMD_H
+#define DAMENDAEMON_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DD_ABI_VERSION 1
+
+enum dd_dtype { DD_F32 = 0, DD_F16 = 1, DD_BF16 = 2, DD_I8 = 3 };
+
+enum dd_error {
+  DD_OK = 0,
+  DD_EINVAL = 1,       /* bad shape, dtype or argument combination */
+  DD_EUNSUPPORTED = 2, /* valid request this build has no kernel for */
+  DD_ELAUNCH = 3,      /* HIP launch error (hipGetLastError after launch) */
+  DD_ESCRATCH = 4      /* caller scratch buffers too small */
+};
+
+/* ABI version; callers refuse a library whose version differs
+ * (native_q4.py:12-15 does the same for the reference's Q4 library). */
+int dd_abi_version(void);
+const char *dd_error_string(int code);
+
+/*
+ * Split-KV size the decode kernel will use for a given maximum context
+ * (page-table width * page size, or the slotted context).  The caller sizes
+ * `partial` as (batch*heads, splits, dim) fp32 and `lse` as
+ * (batch*heads, splits) fp32 from it.  Replaces the host-side split choice
+ * of damendaemon/kernels.py:231-236 (BLOCK/splits).
+ * Returns the number of splits (>=1), or -DD_EINVAL for bad arguments;
+ * *split_tokens receives the tokens per split (a multiple of 64).
+ * `batch_kv` = batch * kv_heads.
+ */
+int dd_decode_splits(int max_context, int batch_kv, int *split_tokens);
+
+/*
+ * Ragged decode attention, one query row per sequence.
+ * Replaces damendaemon/kernels.py:213-267 (`attention` with the `_attention`
+ * and `_merge` Triton kernels), paged (page_table != NULL) or slotted.
+ *
+ *   q          (batch, heads, dim)           q_dtype (F32/F16/BF16)
+ *   k, v       paged: (capacity, kv_heads, page_size, dim) planes,
+ *              slotted: (slots, kv_heads, context, dim)     kv_dtype
+ *   k_scale,   int8 KV only: fp16 scales (..., page_size|context, dim/group)
+ *   v_scale    with the same leading layout as k/v; NULL otherwise
+ *   group      int8 channel group (a divisor of dim, multiple of 32 or ==dim)
+ *   positions  int64 (batch,)  index of the current token; keys 0..pos
+ *   slots      int64 (batch,)  slot / page-table row per sequence, or NULL
+ *   page_table int32 (table_rows, table_width); NULL selects slotted mode;
+ *              a slot outside [0, table_rows) reads no keys
+ *   page_size  tokens per page (paged, a multiple of 16) or context (slotted)
+ *   capacity   physical pages (paged) or slots (slotted): table entries or
+ *              slot ids outside [0, capacity) are treated as unallocated
+ *   window     0 = full causal history, else keys > pos - window only
+ *   scale      softmax scale applied to q.k
+ *   alibi      fp32 (heads,) slope per head or NULL       (kernels.py:160-161)
+ *   rel_bias   fp32 (heads, rel_buckets) T5 bias or NULL   (kernels.py:162-167)
+ *   rel_denom  log(max_distance / (rel_buckets/2))
+ *   sinks      fp32 (heads,) sink logit per head or NULL   (kernels.py:170-175)
+ *   out        (batch, heads, dim) q_dtype
+ *   partial    fp32 (batch*heads, splits, dim)  scratch (unused if splits==1)
+ *   lse        fp32 (batch*heads, splits)       scratch (unused if splits==1)
+ *   splits, split_tokens  from dd_decode_splits()
+ */
+int dd_decode_attention(const void *q, int q_dtype, const void *k,
+                        const void *v, int kv_dtype, const void *k_scale,
+                        const void *v_scale, int group,
+                        const int64_t *positions, const int64_t *slots,
+                        const int32_t *page_table, int table_rows,
+                        int table_width, int batch, int heads, int kv_heads, int dim,
+                        int page_size, int64_t capacity, int window,
+                        float scale,
+                        const float *alibi, const float *rel_bias,
+                        int rel_buckets, float rel_denom, const float *sinks,
+                        void *out, float *partial, float *lse, int splits,
+                        int split_tokens, void *stream);
+
+/*
+ * The two launches of dd_decode_attention, callable one at a time with the
+ * same arguments: dd_decode_partials runs the split kernel (with splits==1
+ * it writes `out` directly); dd_decode_merge runs the log-sum-exp combine
+ * of kernels.py:191-210 (a no-op when splits==1).  Calling both in order
+ * on one stream equals dd_decode_attention; they exist so a caller can
+ * time or overlap the phases separately.
+ */
+int dd_decode_partials(const void *q, int q_dtype, const void *k,
+                       const void *v, int kv_dtype, const void *k_scale,
+                       const void *v_scale, int group,
+                       const int64_t *positions, const int64_t *slots,
+                       const int32_t *page_table, int table_rows,
+                       int table_width, int batch, int heads, int kv_heads,
+                       int dim, int page_size, int64_t capacity, int window,
+                       float scale, const float *alibi, const float *rel_bias,
+                       int rel_buckets, float rel_denom, const float *sinks,
+                       void *out, float *partial, float *lse, int splits,
+                       int split_tokens, void *stream);
+int dd_decode_merge(const void *q, int q_dtype, const void *k, const void *v,
+                    int kv_dtype, const void *k_scale, const void *v_scale,
+                    int group, const int64_t *positions, const int64_t *slots,
+                    const int32_t *page_table, int table_rows,
+                    int table_width, int batch, int heads, int kv_heads,
+                    int dim, int page_size, int64_t capacity, int window,
+                    float scale, const float *alibi, const float *rel_bias,
+                    int rel_buckets, float rel_denom, const float *sinks,
+                    void *out, float *partial, float *lse, int splits,
+                    int split_tokens, void *stream);
+
+/*
+ * Q8_0 KV codec (damendaemon/kv_quant.py:48-76), bit-exact with the
+ * reference's torch arithmetic.  x / out: (rows, dim) in x_dtype/out_dtype
+ * (F32/F16/BF16); q: (rows, dim) int8; scale: (rows, dim/group) fp16.
+ */
+int dd_quantize_q8(const void *x, int x_dtype, int64_t rows, int dim,
+                   int group, void *q, void *scale, void *stream);
+int dd_dequantize_q8(const void *q, const void *scale, int64_t rows, int dim,
+                     int group, void *out, int out_dtype, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DAMENDAEMON_AMD_H */

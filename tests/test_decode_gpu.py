@@ -1,0 +1,240 @@
+"""Decode attention on the GPU against the CPU oracle.
+
+Cases restate the reference's GPU verification recipes as our own tests:
+fragmented paging with NaN-filled pools (scripts/verify_paged_kernels.py:9-69),
+slotted caches with reordered slots, NaN tails and expired windows
+(scripts/verify_kernels.py:33-90), plus the BASELINE configurations.
+
+Tolerances (max |gpu - oracle|, oracle in float64):
+  fp32 KV: 2e-5 + 1e-5*|ref|;  fp16/bf16 KV: 2e-3 + 4e-3*|ref| (the relative
+  term is the output's own bf16 half-ulp);  int8 KV: 5e-3 + 4e-3*|ref|.
+"""
+import math
+
+import pytest
+import torch
+
+from damendaemon_amd import kernels
+from damendaemon_amd.workloads import paged_decode_case, uniform_contexts
+from oracle import paged_oracle as oracle
+
+pytestmark = pytest.mark.gpu
+DEV = 'cuda'
+TOL = {torch.float32: (2e-5, 1e-5), torch.float16: (2e-3, 4e-3), torch.bfloat16: (2e-3, 4e-3),
+       torch.int8: (5e-3, 4e-3)}
+
+
+def check(actual, expected, kind, rows=None):
+    atol, rtol = TOL[kind]
+    a = actual.detach().cpu().double()
+    e = expected.double()
+    if rows is not None:
+        a, e = a[rows], e[rows]
+    assert torch.isfinite(a).all(), 'non-finite output'
+    err = (a - e).abs()
+    bound = atol + rtol * e.abs()
+    worst = (err - bound).max().item()
+    assert worst <= 0, f'max abs err {err.max().item():.3e} exceeds {atol}+{rtol}*|ref|'
+    return err.max().item()
+
+
+def to_dev(case):
+    return {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+
+
+def run_case(case, **kw):
+    d = to_dev(case)
+    return kernels.attention(d['query'], d['cache_k'], d['cache_v'], d['positions'], d['slots'],
+                             page_table=d['page_table'], k_scale=d.get('k_scale'),
+                             v_scale=d.get('v_scale'), **kw)
+
+
+def oracle_case(case, **kw):
+    return oracle.decode_attention(case['query'], case['cache_k'], case['cache_v'], case['positions'],
+                                   case['slots'], page_table=case['page_table'],
+                                   k_scale=case.get('k_scale'), v_scale=case.get('v_scale'), **kw)
+
+
+def test_config_c1_fp32():
+    case = paged_decode_case([17, 128, 300, 1000], 8, 2, 128, torch.float32, seed=1, capacity=128)
+    check(run_case(case), oracle_case(case), torch.float32)
+
+
+@pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize('dim', [64, 96, 128])
+@pytest.mark.parametrize('window', [0, 33])
+def test_fragmented_pages_nan_pool(dtype, dim, window):
+    """verify_paged_kernels.py recipe: 80-page NaN pool, table (4,33), slots [3,0,2]."""
+    torch.manual_seed(2026)
+    heads, kh, page, cap = 8, 2, 16, 80
+    slots = torch.tensor([3, 0, 2])
+    pos = torch.tensor([15, 256, 512])
+    table = torch.full((4, 33), -1, dtype=torch.int32)
+    k = torch.full((cap, kh, page, dim), float('nan'))
+    v = torch.full_like(k, float('nan'))
+    free = torch.randperm(cap).tolist()
+    for slot, p in zip(slots.tolist(), pos.tolist()):
+        for first in range(0, p + 1, page):
+            block = free.pop()
+            table[slot, first // page] = block
+            n = min(page, p + 1 - first)
+            k[block, :, :n] = torch.randn(kh, n, dim)
+            v[block, :, :n] = torch.randn(kh, n, dim)
+    q = torch.randn(3, heads, 1, dim)
+    case = {'query': q.to(dtype), 'cache_k': k.to(dtype), 'cache_v': v.to(dtype), 'page_table': table,
+            'positions': pos, 'slots': slots}
+    check(run_case(case, window=window), oracle_case(case, window=window), dtype)
+
+
+@pytest.mark.parametrize('dim', [64, 96, 128])
+@pytest.mark.parametrize('context', [256, 513, 1024])
+def test_slotted_positions_gqa7(dim, context):
+    """verify_kernels.py:33-55: 14 query heads over 2 KV heads, several positions."""
+    torch.manual_seed(7)
+    heads, kvh = 14, 2
+    k = torch.randn(1, kvh, context, dim).half()
+    v = torch.randn_like(k)
+    q = torch.randn(1, heads, 1, dim).half()
+    kd, vd, qd = k.to(DEV), v.to(DEV), q.to(DEV)
+    for position in sorted({0, 1, 31, min(255, context - 1), min(256, context - 1), context - 1}):
+        pos = torch.tensor([position])
+        out = kernels.attention(qd, kd, vd, pos.to(DEV))
+        check(out, oracle.decode_attention(q, k, v, pos), torch.float16)
+    # entries past the live prefix must not influence the output
+    k[:, :, 1:] = float('nan')
+    v[:, :, 1:] = float('nan')
+    pos = torch.tensor([0])
+    out = kernels.attention(q.to(DEV), k.to(DEV), v.to(DEV), pos.to(DEV))
+    expected = v[:, :, :1].repeat_interleave(heads // kvh, dim=1)
+    assert torch.equal(out.cpu(), expected)
+
+
+def test_slotted_reordered_slots_nan_tails():
+    """verify_kernels.py:56-70."""
+    torch.manual_seed(11)
+    context, dim, heads, kvh = 1024, 64, 14, 2
+    k = torch.randn(5, kvh, context, dim).half()
+    v = torch.randn_like(k)
+    q = torch.randn(4, heads, 1, dim).half()
+    slots = torch.tensor([4, 1, 3, 0])
+    pos = torch.tensor([0, 256, 512, 1023])
+    for s, p in zip(slots.tolist(), pos.tolist()):
+        k[s, :, p + 1:] = float('nan')
+        v[s, :, p + 1:] = float('nan')
+    out = kernels.attention(q.to(DEV), k.to(DEV), v.to(DEV), pos.to(DEV), slots.to(DEV))
+    check(out, oracle.decode_attention(q, k, v, pos, slots), torch.float16)
+
+
+@pytest.mark.parametrize('dtype', [torch.float16, torch.float32])
+@pytest.mark.parametrize('window', [1, 127, 256, 512])
+def test_window_skips_expired_nan(dtype, window):
+    """verify_kernels.py:72-90: D=256, one KV head, expired keys are NaN."""
+    torch.manual_seed(window)
+    dim, heads, context = 256, 4, 2048
+    k = torch.randn(4, 1, context, dim, dtype=dtype)
+    v = torch.randn_like(k)
+    q = torch.randn(4, heads, 1, dim, dtype=dtype)
+    slots = torch.tensor([3, 0, 2, 1])
+    pos = torch.tensor([0, 511, 512, 2047])
+    expected = oracle.decode_attention(q, k, v, pos, slots, window=window, scale=.07)
+    for s, p in zip(slots.tolist(), pos.tolist()):
+        start = max(0, p - window + 1)
+        k[s, :, :start] = float('nan')
+        v[s, :, :start] = float('nan')
+        k[s, :, p + 1:] = float('nan')
+        v[s, :, p + 1:] = float('nan')
+    out = kernels.attention(q.to(DEV), k.to(DEV), v.to(DEV), pos.to(DEV), slots.to(DEV), window=window, scale=.07)
+    check(out, expected, dtype)
+
+
+@pytest.mark.parametrize('heads,kvh', [(4, 4), (6, 3), (16, 1), (24, 8), (32, 8), (12, 4)])
+def test_group_sizes(heads, kvh):
+    case = paged_decode_case([1, 15, 16, 17, 700, 2049], heads, kvh, 128, torch.bfloat16, seed=heads * 10 + kvh,
+                             nan_fill=True)
+    check(run_case(case), oracle_case(case), torch.bfloat16)
+
+
+@pytest.mark.parametrize('group', [32, 128])
+@pytest.mark.parametrize('qdtype', [torch.bfloat16, torch.float16])
+def test_int8_pages(group, qdtype):
+    case = paged_decode_case([5, 64, 333, 1500, 4000], 32, 8, 128, torch.float32, seed=group, nan_fill=False)
+    qk, ks = oracle.quantize_q8(case['cache_k'], group)
+    qv, vs = oracle.quantize_q8(case['cache_v'], group)
+    case.update(cache_k=qk, cache_v=qv, k_scale=ks, v_scale=vs, query=case['query'].to(qdtype))
+    check(run_case(case), oracle_case(case), torch.int8)
+
+
+def test_int8_dim256_group32():
+    case = paged_decode_case([40, 900, 3000], 16, 2, 256, torch.float32, seed=3)
+    qk, ks = oracle.quantize_q8(case['cache_k'], 32)
+    qv, vs = oracle.quantize_q8(case['cache_v'], 32)
+    case.update(cache_k=qk, cache_v=qv, k_scale=ks, v_scale=vs, query=case['query'].to(torch.bfloat16))
+    check(run_case(case), oracle_case(case), torch.int8)
+
+
+def test_alibi_sinks_relative_bias_with_splits():
+    torch.manual_seed(3)
+    case = paged_decode_case([3, 600, 2500, 5000], 8, 2, 128, torch.float16, seed=9)
+    heads = 8
+    alibi = torch.linspace(-0.01, -0.001, heads)
+    sinks = torch.randn(heads)
+    rel = torch.randn(heads, 32)
+    for kw in ({'alibi': alibi}, {'sinks': sinks}, {'relative_bias': rel, 'relative_max_distance': 128},
+               {'alibi': alibi, 'sinks': sinks, 'window': 300}):
+        dev_kw = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in kw.items()}
+        check(run_case(case, **dev_kw), oracle_case(case, **kw), torch.float16)
+
+
+def test_sinks_single_split():
+    case = paged_decode_case([3, 60, 100], 4, 2, 64, torch.float16, seed=4)
+    sinks = torch.tensor([0.5, -1.0, 2.0, 0.0])
+    check(run_case(case, sinks=sinks.to(DEV)), oracle_case(case, sinks=sinks), torch.float16)
+
+
+def test_page_relocation_is_bitwise_invariant():
+    """Moving pages to other physical slots (and rewriting the table) must not change a bit."""
+    case = paged_decode_case([100, 2000, 4097], 32, 8, 128, torch.bfloat16, seed=12)
+    out1 = run_case(case)
+    cap = case['capacity']
+    perm = torch.randperm(cap, generator=torch.Generator().manual_seed(1))
+    moved = dict(case)
+    moved['cache_k'] = torch.empty_like(case['cache_k'])
+    moved['cache_v'] = torch.empty_like(case['cache_v'])
+    moved['cache_k'][perm] = case['cache_k']
+    moved['cache_v'][perm] = case['cache_v']
+    t = case['page_table'].long()
+    moved['page_table'] = torch.where(t >= 0, perm[t.clamp_min(0)], t).to(torch.int32)
+    out2 = run_case(moved)
+    assert torch.equal(out1, out2)
+
+
+def test_scratch_bytes_partitions_rows():
+    case = paged_decode_case([700, 50, 1800, 33, 900], 8, 2, 128, torch.float16, seed=21)
+    part = run_case(case, scratch_bytes=8 * (4 * (128 + 1) * 4 + 128 * 2) * 2)
+    check(part, oracle_case(case), torch.float16)
+
+
+def test_config_c2_bf16_rows():
+    """Full 64-sequence bf16 decode; oracle on a row subset (the full oracle is minutes of CPU)."""
+    contexts = uniform_contexts(64, 512, 8192, 2)
+    case = paged_decode_case(contexts, 32, 8, 128, torch.bfloat16, seed=2, device=DEV, table_width=512)
+    out = kernels.attention(case['query'], case['cache_k'], case['cache_v'], case['positions'], case['slots'],
+                            page_table=case['page_table'])
+    rows = [0, 17, 42, 63]
+    cpu = {k: (v.cpu() if torch.is_tensor(v) else v) for k, v in case.items()}
+    expected = oracle_case(cpu, rows=rows)
+    err = check(out, expected, torch.bfloat16, rows=rows)
+    assert err <= 2e-3
+
+
+def test_config_c5_long_context_outliers():
+    """16 x 32768 tokens, D=256, 8 query heads per KV head, 1% K outliers x8."""
+    ctx = [32768] * 16
+    case = paged_decode_case(ctx, 16, 2, 256, torch.bfloat16, seed=5, device=DEV, capacity=16 * 2048,
+                             outlier_frac=0.01)
+    out = kernels.attention(case['query'], case['cache_k'], case['cache_v'], case['positions'], case['slots'],
+                            page_table=case['page_table'])
+    rows = [0, 9]
+    cpu = {k: (v.cpu() if torch.is_tensor(v) else v) for k, v in case.items()}
+    expected = oracle_case(cpu, rows=rows)
+    check(out, expected, torch.bfloat16, rows=rows)

@@ -1,0 +1,48 @@
+"""The C-ABI library loads on a CPU-only host and exports every symbol the header declares."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / 'include' / 'damendaemon_amd.h'
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    return sorted(set(re.findall(r'\b(dd_[a-z0-9_]+)\s*\(', text)))
+
+
+def test_header_declares_entry_points():
+    names = declared_symbols()
+    assert 'dd_abi_version' in names and 'dd_decode_attention' in names
+
+
+def test_library_exports_every_declared_symbol():
+    from damendaemon_amd import _native
+    if not _native.LIBRARY.exists():
+        pytest.fail('library not built: run python -m damendaemon_amd.build')
+    lib = ctypes.CDLL(str(_native.LIBRARY))
+    missing = [n for n in declared_symbols() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_abi_version_and_python_signatures():
+    from damendaemon_amd import _native
+    lib = _native.library()
+    assert lib.dd_abi_version() == _native.ABI_VERSION
+    assert set(_native.SIGNATURES) <= set(declared_symbols())
+    assert lib.dd_error_string(1) == b'invalid argument'
+
+
+def test_split_policy_covers_context():
+    from damendaemon_amd import _native
+    lib = _native.library()
+    for ctx, bkh in [(1024, 8), (8192, 512), (32768, 32), (16, 1), (513, 3)]:
+        tokens = ctypes.c_int()
+        splits = lib.dd_decode_splits(ctx, bkh, ctypes.byref(tokens))
+        assert splits >= 1 and tokens.value % 64 == 0
+        assert splits * tokens.value >= ctx > (splits - 1) * tokens.value
+    assert lib.dd_decode_splits(0, 1, None) < 0

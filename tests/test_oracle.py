@@ -1,0 +1,139 @@
+"""Pin the CPU oracle against things other than itself (library routines,
+closed forms, known answers, brute force), so a dropped term, wrong index or
+transposed operand in the oracle fails here before any GPU comparison."""
+import math
+
+import pytest
+import torch
+from torch.nn import functional as F
+
+from damendaemon_amd.workloads import paged_decode_case
+from oracle import paged_oracle as O
+
+
+def test_gather_matches_page_concatenation():
+    """scripts/verify_paged_copies.py:15-24 builds the expected dense tensor with torch.cat."""
+    g = torch.Generator().manual_seed(927)
+    for length in (1, 15, 16, 17, 127, 513):
+        pages = torch.randperm(40, generator=g)[:(length + 15) // 16]
+        table = torch.full((4, 33), -1, dtype=torch.int32)
+        table[3, :len(pages)] = pages.to(torch.int32)
+        cache = torch.randn((2, 40, 3, 16, 96), generator=g)
+        dense = O.copy_pages(cache, table, 3, length)
+        expected = torch.cat([cache[:, p] for p in pages.tolist()], dim=2)[:, :, :length]
+        assert torch.equal(dense, expected)
+        restored = O.copy_pages(torch.full_like(cache, 17.), table, 3, length, snapshot=dense)
+        wanted = torch.full_like(cache, 17.)
+        for block, p in enumerate(pages.tolist()):
+            n = min(16, length - 16 * block)
+            wanted[:, p, :, :n] = expected[:, :, 16 * block:16 * block + n]
+        assert torch.equal(restored, wanted)
+
+
+def test_quantize_known_answers():
+    x = torch.zeros(2, 64)
+    x[0, :32] = torch.linspace(-3, 3, 32)
+    x[1, 32:] = 0.5
+    q, s = O.quantize_q8(x, 32)
+    assert s.dtype == torch.float16 and s.shape == (2, 2)
+    assert s[0, 1] == 0 and (q[0, 32:] == 0).all()            # zero group -> zero scale, zero data
+    assert s[1, 0] == 0 and (q[1, :32] == 0).all()
+    assert q[0, 0] == -127 and q[0, 31] == 127                 # +-absmax -> +-127
+    assert (q[1, 32:] == 127).all()
+    assert s[0, 0] == torch.tensor(3 / 127).half()
+    # exact halves round away from zero: scale 1 -> x/1
+    y = torch.tensor([[127.0, 0.5, -0.5, 1.5, -2.5, 2.4999] + [0.0] * 26])
+    qy, sy = O.quantize_q8(y, 32)
+    assert float(sy[0, 0]) == 1.0
+    assert qy[0, :6].tolist() == [127, 1, -1, 2, -3, 2]
+
+
+def test_quantize_error_bound_and_dequant():
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(50, 128, generator=g) * 3
+    for group in (32, 64, 128):
+        q, s = O.quantize_q8(x, group)
+        back = O.dequantize_q8(q, s)
+        sc = s.float().repeat_interleave(group, -1)
+        # half a quantisation step, plus the fp16 rounding of the scale itself
+        bound = sc / 2 + x.abs() * 2 ** -10 + 1e-7
+        assert ((back - x).abs() <= bound).all()
+    d = torch.tensor([[1, -2, 127, -127]], dtype=torch.int8)
+    assert O.dequantize_q8(d, torch.tensor([[0.5]], dtype=torch.float16)).tolist() == [[0.5, -1.0, 63.5, -63.5]]
+
+
+def _dense(case, b):
+    pos = int(case['positions'][b])
+    slot = int(case['slots'][b])
+    k = torch.cat([case['cache_k'][int(p)] for p in case['page_table'][slot] if p >= 0], dim=1)[:, :pos + 1]
+    v = torch.cat([case['cache_v'][int(p)] for p in case['page_table'][slot] if p >= 0], dim=1)[:, :pos + 1]
+    return k, v
+
+
+def test_decode_matches_sdpa_library():
+    case = paged_decode_case([1, 17, 130, 400], 8, 2, 64, torch.float32, seed=4)
+    out = O.decode_attention(case['query'], case['cache_k'], case['cache_v'], case['positions'], case['slots'],
+                             page_table=case['page_table'])
+    for b in range(4):
+        k, v = _dense(case, b)
+        ref = F.scaled_dot_product_attention(case['query'][b:b + 1].double(), k[None].double(), v[None].double(),
+                                             enable_gqa=True)
+        assert torch.allclose(out[b:b + 1], ref, atol=1e-12)
+
+
+def test_decode_alibi_window_match_sdpa_with_mask():
+    case = paged_decode_case([50, 333], 4, 2, 64, torch.float32, seed=5)
+    alibi = torch.tensor([-0.1, -0.05, 0.02, 0.0])
+    out = O.decode_attention(case['query'], case['cache_k'], case['cache_v'], case['positions'], case['slots'],
+                             page_table=case['page_table'], alibi=alibi, window=40, scale=0.3)
+    for b in range(2):
+        k, v = _dense(case, b)
+        n = k.shape[1]
+        t = torch.arange(n, dtype=torch.float64)
+        bias = alibi.double()[:, None] * t[None, :]
+        bias = torch.where(t[None, :] > n - 1 - 40, bias, torch.tensor(-math.inf, dtype=torch.float64))
+        ref = F.scaled_dot_product_attention(case['query'][b:b + 1].double(), k[None].double(), v[None].double(),
+                                             attn_mask=bias[None, :, None, :], enable_gqa=True, scale=0.3)
+        assert torch.allclose(out[b:b + 1], ref, atol=1e-12)
+
+
+def test_decode_special_cases():
+    case = paged_decode_case([1, 64, 200], 4, 4, 32, torch.float32, seed=6)
+    args = (case['query'], case['cache_k'], case['cache_v'], case['positions'], case['slots'])
+    base = O.decode_attention(*args, page_table=case['page_table'])
+    # one live key -> its value vector
+    assert torch.allclose(base[0, :, 0], case['cache_v'][int(case['page_table'][0, 0]), :, 0].double())
+    # a window covering the context changes nothing; a sink of -inf changes nothing; zero alibi changes nothing
+    for kw in ({'window': 10 ** 6}, {'sinks': torch.full((4,), -math.inf)}, {'alibi': torch.zeros(4)}):
+        assert torch.allclose(O.decode_attention(*args, page_table=case['page_table'], **kw), base, atol=1e-12)
+    # constant V rows -> that constant
+    cv = torch.ones_like(case['cache_v']) * 0.25
+    out = O.decode_attention(case['query'], case['cache_k'], cv, case['positions'], case['slots'],
+                             page_table=case['page_table'])
+    assert torch.allclose(out, torch.full_like(out, 0.25))
+    # a sink of s shrinks the output by sum(w)/(sum(w)+e^s): check on a single key, logit irrelevant
+    s = torch.tensor([0.0, 1.0, -1.0, 2.0])
+    out = O.decode_attention(*args, page_table=case['page_table'], sinks=s)
+    k, v = _dense(case, 0)
+    logit = (case['query'][0, :, 0] * k[:, 0]).sum(-1) * 32 ** -.5
+    factor = 1 / (1 + torch.exp(s - logit))
+    assert torch.allclose(out[0, :, 0], (v[:, 0] * factor[:, None]).double(), atol=1e-6)
+
+
+def test_t5_bucket_matches_transformers():
+    t5 = pytest.importorskip('transformers.models.t5.modeling_t5')
+    for buckets, maxd in ((32, 128), (8, 20), (64, 300)):
+        rel = -torch.arange(0, 2000)[None, :]          # memory - query = t - pos <= 0
+        lib = t5.T5Attention._relative_position_bucket(rel, bidirectional=False, num_buckets=buckets,
+                                                       max_distance=maxd)[0].tolist()
+        ours = [O.t5_bucket(n, buckets, maxd) for n in range(2000)]
+        assert ours == lib
+
+
+def test_sdpa_baseline_agrees_with_oracle():
+    case = paged_decode_case([5, 40, 300, 77], 8, 2, 64, torch.float32, seed=8)
+    a = O.decode_attention(case['query'], case['cache_k'], case['cache_v'], case['positions'], case['slots'],
+                           page_table=case['page_table'])
+    b = O.decode_attention_sdpa(case['query'], case['cache_k'], case['cache_v'], case['positions'], case['slots'],
+                                case['page_table'])
+    assert torch.allclose(a.float(), b, atol=2e-5)
