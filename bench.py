@@ -40,6 +40,19 @@ def algorithmic_bytes(case, kv_bytes_per_token_head):
     return ctx * KH * kv_bytes_per_token_head + q_o + pages * 4
 
 
+def measured_traffic(config):
+    """HBM bytes per launch of the split kernel from the committed rocprofv3
+    PMC summary (FETCH_SIZE + WRITE_SIZE, calibrated against a plain copy),
+    or None when no summary exists for this workload."""
+    path = os.path.join(ROOT, 'profiles', f'decode_{config}_bf16_pmc.md')
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith('traffic_bytes_per_launch:'):
+            return int(line.split(':')[1])
+    return None
+
+
 def build_case(name, device):
     from damendaemon_amd import workloads, kv_quant
     if name == 'c2':
@@ -101,7 +114,17 @@ def main():
     ap.add_argument('--warmup', type=int, default=5)
     ap.add_argument('--config', default='c2', choices=['c2', 'c3', 'c5'])
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--copy-probe', action='store_true',
+                    help='only run 1 GiB device-to-device copies (calibrates rocprofv3 FETCH/WRITE_SIZE)')
     args = ap.parse_args()
+    if args.copy_probe:
+        src = torch.randn(1 << 28, device='cuda:0')      # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({'copy_probe_bytes_each_way': src.numel() * 4, 'copies': 5}))
+        return
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU only: this build has no multi-GPU path '
               '(decode shards by sequence with no exchange; see the design notes)', file=sys.stderr)
@@ -152,7 +175,7 @@ def main():
                    'split_kernel_ms': split_ms, 'merge_kernel_ms': merge_ms,
                    'step_hbm_gbps': nbytes / (ms_per_step * 1e-3) / 1e9},
         'roofline': {'bound': 'hbm', 'achieved': achieved, 'peak': PEAK_HBM_GBPS, 'unit': 'GB/s',
-                     'frac': achieved / PEAK_HBM_GBPS, 'traffic': None, 'algorithmic_bytes': nbytes},
+                     'frac': achieved / PEAK_HBM_GBPS, 'traffic': measured_traffic(args.config), 'algorithmic_bytes': nbytes},
         'cpu_baseline': None if args.no_cpu_baseline else cpu_baseline(case),
     }
     print(json.dumps(line), flush=True)

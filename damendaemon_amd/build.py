@@ -23,8 +23,8 @@ FLAGS = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}',
          '-Wno-unused-command-line-argument']
 
 
-def _compile(source, obj):
-    cmd = [HIPCC, *FLAGS, '-c', str(source), '-o', str(obj)]
+def _compile(source, obj, extra=()):
+    cmd = [HIPCC, *FLAGS, *extra, '-c', str(source), '-o', str(obj)]
     run = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = '\n'.join(l for l in run.stderr.splitlines() if noise not in l)
@@ -33,24 +33,28 @@ def _compile(source, obj):
     return err
 
 
-def build(jobs=None, verbose=False):
+def build(jobs=None, verbose=False, extra_flags=(), library=LIBRARY):
+    """Compile and link; ``extra_flags`` (e.g. -D tuning macros) and
+    ``library`` allow side-by-side variant builds."""
+    library = Path(library)
     OUT_DIR.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob('*.hip'))
-    objs = [OUT_DIR / (s.stem + '.o') for s in sources]
+    tag = library.stem
+    objs = [OUT_DIR / f'{s.stem}.{tag}.o' for s in sources]
     jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 4)), 16)
     with ThreadPoolExecutor(jobs) as pool:
-        for warn in pool.map(_compile, sources, objs):
+        for warn in pool.map(lambda s, o: _compile(s, o, extra_flags), sources, objs):
             if warn and verbose:
                 print(warn, file=sys.stderr)
-    tmp = LIBRARY.with_suffix('.so.tmp')
+    tmp = library.with_suffix('.so.tmp')
     link = [HIPCC, '-shared', f'--offload-arch={ARCH}', *map(str, objs), '-o', str(tmp)]
     run = subprocess.run(link, capture_output=True, text=True)
     if run.returncode:
         raise RuntimeError('link failed:\n' + run.stderr)
-    os.replace(tmp, LIBRARY)
+    os.replace(tmp, library)
     for o in objs:
         o.unlink()
-    return LIBRARY
+    return library
 
 
 if __name__ == '__main__':

@@ -12,11 +12,12 @@ extern template int dd_decode::dispatch_d<DD_I8, DD_F16>(const DecodeParams &, i
 
 extern "C" int dd_decode_splits(int max_context, int batch_kv, int *split_tokens) {
   if (max_context <= 0 || batch_kv <= 0) return -DD_EINVAL;
-  // Enough workgroups to cover 256 CUs several times over, but at least
-  // 256 keys per split so the per-split fixed cost stays small.
-  int st = 512;
-  while (st > 256 && (long)batch_kv * dd_cdiv(max_context, st) < 2048) st >>= 1;
-  while (st < 8192 && (long)batch_kv * dd_cdiv(max_context, st) > 16384) st <<= 1;
+  // About eight splits over the longest possible context, 256..2048 keys
+  // each: long enough that the per-split setup and the merge stay small,
+  // short enough that ragged batches balance over the 256 CUs.  Splits are
+  // dispatched split-major, so unused trailing splits cost one early exit.
+  int st = 256;
+  while (st < 2048 && st * 8 < max_context) st <<= 1;
   if (split_tokens) *split_tokens = st;
   return (int)dd_cdiv(max_context, st);
 }
@@ -67,6 +68,9 @@ static int decode_entry(int phase, const void *q, int q_dtype, const void *k, co
   if (p.paged) {
     if (table_width <= 0 || page_size % 16) return DD_EUNSUPPORTED;
     p.ctx_limit = table_width * page_size;
+    p.chunk_shift = 0;
+    while ((16 << p.chunk_shift) < page_size) ++p.chunk_shift;
+    if ((16 << p.chunk_shift) != page_size) return DD_EUNSUPPORTED;
   } else {
     p.ctx_limit = page_size;
   }

@@ -53,9 +53,16 @@ struct DecodeParams {
   float rel_denom;
   float scale_log2;
   int paged;
+  int chunk_shift;  // log2(page / 16) for paged caches
 };
 
 constexpr int kWaves = 4;
+#ifndef DD_DECODE_PREFETCH
+#define DD_DECODE_PREFETCH 0
+#endif
+// Load the next page into a second register set while consuming the current
+// one (costs occupancy; off unless measured to win).
+constexpr bool kPrefetch = DD_DECODE_PREFETCH;
 constexpr float kNegInf = -__builtin_inff();
 
 // Element offset of the first token of 16-token chunk `pg` of (row, kh), or
@@ -63,15 +70,19 @@ constexpr float kNegInf = -__builtin_inff();
 DD_DEV long chunk_base(const DecodeParams &p, int row, int kh, int pg, int D) {
   if (p.paged) {
     if (row < 0 || row >= p.table_rows) return -1;
-    const int tok = pg * 16;
-    const int entry = tok / p.page;
+    const int entry = pg >> p.chunk_shift;
+    const int within = (pg - (entry << p.chunk_shift)) * 16;
     const long phys = p.table[(long)row * p.table_w + entry];
     if (phys < 0 || phys >= p.capacity) return -1;
-    return ((phys * p.KH + kh) * (long)p.page + (tok % p.page)) * (long)D;
+    return ((phys * p.KH + kh) * (long)p.page + within) * (long)D;
   }
   if (row < 0 || row >= p.capacity) return -1;
   return (((long)row * p.KH + kh) * (long)p.page + (long)pg * 16) * (long)D;
 }
+
+// 2^x on the hardware exp unit (inputs here are <= 0 or -inf; results that
+// would be denormal only weight negligible terms).
+DD_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Convert 8 signed bytes to 8 exact bf16 / f16 MFMA operands.
 template <int QT>
@@ -135,8 +146,14 @@ DD_DEV int rel_bucket(int distance, int buckets, float denom) {
   return large < buckets - 1 ? large : buckets - 1;
 }
 
+#ifdef DD_DECODE_WAVES_PER_EU
+#define DD_DECODE_ATTR __attribute__((amdgpu_waves_per_eu(DD_DECODE_WAVES_PER_EU)))
+#else
+#define DD_DECODE_ATTR
+#endif
+
 template <int KVT, int QT, int D, int GB>
-__global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
+__global__ __launch_bounds__(256) DD_DECODE_ATTR void decode_kernel(DecodeParams p) {
   constexpr bool kMfma = KVT != DD_F32;
   constexpr int VE = KVT == DD_F32 ? 4 : (KVT == DD_I8 ? 16 : 8);  // V elems per 16 B
   constexpr int LPT = D / VE;                                       // lanes per V token
@@ -157,26 +174,29 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   const int tl = lane & 15;
   const int G = p.G;
 
+  // Split-major order: every sequence's first split is dispatched before any
+  // second split, so full-length splits run first and the short (or empty)
+  // final splits fill the tail of the launch.
   const int wg = blockIdx.x;
-  const int split = wg % p.splits;
-  const int bkh = wg / p.splits;
+  const int nbkh = p.B * p.KH;
+  const int split = wg / nbkh;
+  const int bkh = wg - split * nbkh;
   const int b = bkh / p.KH;
   const int kh = bkh % p.KH;
 
-  const long pos = p.pos[b];
+  const long pos64 = p.pos[b];
   const int row = p.slots ? (int)p.slots[b] : 0;
-  long t_hi = pos + 1;
-  if (t_hi > p.ctx_limit) t_hi = p.ctx_limit;
-  long t_lo = 0;
-  if (p.window > 0 && pos - p.window + 1 > 0) t_lo = pos - p.window + 1;
-  long s_lo = (long)split * p.split_tokens;
-  long s_hi = s_lo + p.split_tokens;
+  int t_hi = pos64 + 1 < p.ctx_limit ? (int)pos64 + 1 : p.ctx_limit;
+  int t_lo = 0;
+  if (p.window > 0 && pos64 - p.window + 1 > 0) t_lo = (int)(pos64 - p.window + 1);
+  int s_lo = split * p.split_tokens;
+  int s_hi = s_lo + p.split_tokens;
   if (s_hi > t_hi) s_hi = t_hi;
   if (s_lo < t_lo) s_lo = t_lo;
   if (s_lo >= s_hi) return;  // empty split: the merge never reads it
 
-  const int pg_first = (int)(s_lo >> 4);
-  const int pg_last = (int)((s_hi - 1) >> 4);
+  const int pg_first = s_lo >> 4;
+  const int pg_last = (s_hi - 1) >> 4;
   const long head0 = (long)b * p.H + (long)kh * G;
 
   // ---- query operand ----------------------------------------------------
@@ -217,69 +237,101 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   const int vdim = VE * (lane % LPT);      // first dim of this lane's V slice
   const bool v_lane_on = lane < LPT * TPI;
 
-  for (int pg = pg_first + w; pg <= pg_last; pg += kWaves) {
+  // Registers of one page: raw K (MFMA layout), raw V (VALU layout) and,
+  // for int8 pages, the per-token scales.  The next page is loaded into a
+  // second set while the current one is consumed.
+  struct PageRegs {
+    long base;
+    u32x4 k[kMfma ? NC : NC4];
+    u32x2 k8[KVT == DD_I8 ? NC : 1];
+    u32x4 v[NIT];
+    float ks[KVT == DD_I8 ? NC : 1];
+    float vs[KVT == DD_I8 ? NIT : 1];
+  };
+  // All loads are unconditional: invalid or missing tokens read a clamped,
+  // always-mapped row (page 0 when the table entry is unallocated, the last
+  // row of the slot for a slotted cache).  Their logits are masked to -inf
+  // and their V rows are zeroed before use.
+  constexpr bool kAllLanes = LPT * TPI == 64 && NIT * TPI == 16;
+  // Per-lane byte offsets inside a 16-token chunk are loop invariant; the
+  // chunk base is wave-uniform, so each load is SGPR base + 32-bit offset.
+  auto load_page = [&](int pg, PageRegs &R) {
     const long base = chunk_base(p, row, kh, pg, D);
-    const long t0 = (long)pg * 16;
-    const long tk = t0 + tl;
-    const bool kval = base >= 0 && tk >= s_lo && tk < s_hi;
-
-    // -- issue K and V loads for the page --
-    u32x4 kraw[kMfma ? NC : NC4];
-    u32x2 kraw8[KVT == DD_I8 ? NC : 1];
+    R.base = base;
+    const long sb = base < 0 ? 0 : base;
+    const int lim = p.paged ? 15 : min(15, p.page - 1 - pg * 16);
+    const unsigned krow = (unsigned)min(tl, lim);
+    const char *kb = kbytes + KB * sb;  // wave-uniform
+    const char *vb = vbytes + KB * sb;
     if constexpr (KVT == DD_I8) {
 #pragma unroll
+      for (int c = 0; c < NC; ++c) R.k8[c] = *(const u32x2 *)(kb + (krow * D + 8 * r + 32 * c));
+      const unsigned short *ksc = p.ks + (sb / D) * p.ngroups;
+#pragma unroll
       for (int c = 0; c < NC; ++c) {
-        kraw8[c] = kval ? *(const u32x2 *)(kbytes + (base + (long)tl * D + 8 * r + 32 * c))
-                        : u32x2{0, 0};
+        R.ks[c] = (c == 0 || p.group != D) ? half_bits_to_float(ksc[krow * p.ngroups + (32 * c) / p.group]) : 0.f;
       }
     } else if constexpr (kMfma) {
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        kraw[c] = kval ? *(const u32x4 *)(kbytes + 2 * (base + (long)tl * D + 8 * r + 32 * c))
-                       : u32x4{0, 0, 0, 0};
-      }
+      for (int c = 0; c < NC; ++c) R.k[c] = *(const u32x4 *)(kb + 2u * (krow * D + 8 * r + 32 * c));
     } else {
 #pragma unroll
-      for (int c = 0; c < NC4; ++c) {
-        kraw[c] = kval ? *(const u32x4 *)(kbytes + 4 * (base + (long)tl * D + 4 * r + 16 * c))
-                       : u32x4{0, 0, 0, 0};
-      }
+      for (int c = 0; c < NC4; ++c) R.k[c] = *(const u32x4 *)(kb + 4u * (krow * D + 4 * r + 16 * c));
     }
-    u32x4 vraw[NIT];
-    bool vval[NIT];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
-      const int tv = it * TPI + vtok_lane;
-      const long t = t0 + tv;
-      vval[it] = v_lane_on && tv < 16 && base >= 0 && t >= s_lo && t < s_hi;
-      vraw[it] = vval[it] ? *(const u32x4 *)(vbytes + KB * (base + (long)tv * D + vdim))
-                          : u32x4{0, 0, 0, 0};
+      const unsigned vrow = (unsigned)min(it * TPI + vtok_lane, lim);
+      R.v[it] = *(const u32x4 *)(vb + KB * (vrow * D + vdim));
+      if constexpr (KVT == DD_I8) R.vs[it] = half_bits_to_float(p.vs[(sb / D) * p.ngroups + vrow * p.ngroups + vdim / p.group]);
+    }
+  };
+
+  PageRegs cur;
+  int pg = pg_first + w;
+  if (pg <= pg_last) load_page(pg, cur);
+  for (; pg <= pg_last; pg += kWaves) {
+    PageRegs nxt;
+    if constexpr (kPrefetch) {
+      if (pg + kWaves <= pg_last) load_page(pg + kWaves, nxt);
+    }
+    const long base = cur.base;
+    const int t0 = pg * 16;
+    const int tk = t0 + tl;
+    const bool kval = base >= 0 && tk >= s_lo && tk < s_hi;
+    if (!kAllLanes || base < 0 || t0 < s_lo || t0 + 16 > s_hi) {
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        const int tv = it * TPI + vtok_lane;
+        const bool vv = v_lane_on && tv < 16 && base >= 0 && t0 + tv >= s_lo && t0 + tv < s_hi;
+        if (!vv) cur.v[it] = u32x4{0, 0, 0, 0};
+        if constexpr (KVT == DD_I8) cur.vs[it] = vv ? cur.vs[it] : 0.f;
+      }
+    }
+    if constexpr (KVT == DD_I8) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) cur.ks[c] = kval ? cur.ks[c] : 0.f;
     }
 
     // -- logits: lane holds token tl for heads 4r+i --
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
     if constexpr (KVT == DD_I8) {
-      const unsigned short *ksc =
-          p.ks + (base / D + tl) * p.ngroups;  // scale row of this lane's token
       if (p.group == D) {
 #pragma unroll
-        for (int c = 0; c < NC; ++c) s = mfma16x16x32<QT>(qa[c], widen_i8x8<QT>(kraw8[c]), s);
-        const float sc = kval ? half_bits_to_float(ksc[0]) : 0.f;
+        for (int c = 0; c < NC; ++c) s = mfma16x16x32<QT>(qa[c], widen_i8x8<QT>(cur.k8[c]), s);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s[i] *= sc;
+        for (int i = 0; i < 4; ++i) s[i] *= cur.ks[0];
       } else {
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-          const f32x4 part = mfma16x16x32<QT>(qa[c], widen_i8x8<QT>(kraw8[c]),
+          const f32x4 part = mfma16x16x32<QT>(qa[c], widen_i8x8<QT>(cur.k8[c]),
                                               f32x4{0.f, 0.f, 0.f, 0.f});
-          const float sc = kval ? half_bits_to_float(ksc[(32 * c) / p.group]) : 0.f;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) s[i] += sc * part[i];
+          for (int i = 0; i < 4; ++i) s[i] += cur.ks[c] * part[i];
         }
       }
     } else if constexpr (kMfma) {
 #pragma unroll
-      for (int c = 0; c < NC; ++c) s = mfma16x16x32<QT>(qa[c], kraw[c], s);
+      for (int c = 0; c < NC; ++c) s = mfma16x16x32<QT>(qa[c], cur.k[c], s);
     } else {
       float part[GB];
 #pragma unroll
@@ -289,8 +341,8 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 #pragma unroll
         for (int h = 0; h < GB; ++h) {
           const float *qrow = &s_q[h < G ? h : 0][4 * r + 16 * c];
-          part[h] += qrow[0] * __uint_as_float(kraw[c][0]) + qrow[1] * __uint_as_float(kraw[c][1]) +
-                     qrow[2] * __uint_as_float(kraw[c][2]) + qrow[3] * __uint_as_float(kraw[c][3]);
+          part[h] += qrow[0] * __uint_as_float(cur.k[c][0]) + qrow[1] * __uint_as_float(cur.k[c][1]) +
+                     qrow[2] * __uint_as_float(cur.k[c][2]) + qrow[3] * __uint_as_float(cur.k[c][3]);
         }
       }
 #pragma unroll
@@ -315,7 +367,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
       float x = s[i] * p.scale_log2;
       if (p.alibi && hg < G) x += p.alibi[head0 - (long)b * p.H + hg] * kLog2e * (float)tk;
       if (p.rel && hg < G) {
-        const long dist = pos - tk > 0 ? pos - tk : 0;
+        const long dist = pos64 - tk > 0 ? pos64 - tk : 0;
         const int bucket = rel_bucket((int)dist, p.rel_buckets, p.rel_denom);
         x += p.rel[(head0 - (long)b * p.H + hg) * p.rel_buckets + bucket] * kLog2e;
       }
@@ -332,7 +384,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     for (int h = 0; h < GB; ++h) {
       const float mb = read_lane(rmax[h & 3], 16 * ((h >> 2) & 3));
       const float mn = fmaxf(m_run[h], mb);
-      alpha[h] = mn == kNegInf ? 1.f : exp2f(m_run[h] - mn);
+      alpha[h] = mn == kNegInf ? 1.f : fast_exp2(m_run[h] - mn);
       m_use[h] = mn == kNegInf ? 0.f : mn;
       rescale |= alpha[h] != 1.f;
       m_run[h] = mn;
@@ -360,7 +412,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
       for (int rr = 1; rr < 4; ++rr) {
         if (4 * rr + i < GB && r == rr) mm = m_use[4 * rr + i];
       }
-      const float pr = exp2f(s[i] - mm);
+      const float pr = fast_exp2(s[i] - mm);
       lsum[i] += pr;
       const int hg = 4 * r + i;
       if (hg < G && hg < GB) s_p[w][tl][hg] = pr;
@@ -370,8 +422,6 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // -- p.v --
-    const unsigned short *vsc = nullptr;
-    if constexpr (KVT == DD_I8) vsc = p.vs + (base >= 0 ? base / D : 0) * p.ngroups + vdim / p.group;
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
       int tv = it * TPI + vtok_lane;
@@ -380,12 +430,11 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 #pragma unroll
       for (int h = 0; h < GB; ++h) pv[h] = s_p[w][tv][h];
       if constexpr (KVT == DD_I8) {
-        const float sc = vval[it] ? half_bits_to_float(vsc[(long)tv * p.ngroups]) : 0.f;
 #pragma unroll
-        for (int h = 0; h < GB; ++h) pv[h] *= sc;
+        for (int h = 0; h < GB; ++h) pv[h] *= cur.vs[it];
       }
       float x[VE];
-      widen_v<KVT, VE>(vraw[it], x);
+      widen_v<KVT, VE>(cur.v[it], x);
 #pragma unroll
       for (int h = 0; h < GB; ++h) {
 #pragma unroll
@@ -395,6 +444,11 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if constexpr (kPrefetch) {
+      cur = nxt;
+    } else if (pg + kWaves <= pg_last) {
+      load_page(pg + kWaves, cur);
+    }
   }
 
   // ---- reduce inside the wave ---------------------------------------------
@@ -454,7 +508,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 #pragma unroll
     for (int ww = 1; ww < kWaves; ++ww) mm = fmaxf(mm, s_ml[ww][0][h]);
     mtot[h] = mm;
-    fac[h] = m_run[h] == kNegInf ? 0.f : exp2f(m_run[h] - mm);
+    fac[h] = m_run[h] == kNegInf ? 0.f : fast_exp2(m_run[h] - mm);
   }
 #pragma unroll
   for (int ww = 0; ww < kWaves; ++ww) {
@@ -481,7 +535,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     float l = 0.f;
     for (int ww = 0; ww < kWaves; ++ww) {
       const float mw = s_ml[ww][0][h];
-      if (mw != kNegInf) l += s_ml[ww][1][h] * exp2f(mw - mm);
+      if (mw != kNegInf) l += s_ml[ww][1][h] * fast_exp2(mw - mm);
     }
     float o = s_o[h][d];
     const long bh = head0 + h;
@@ -489,8 +543,8 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
       if (p.sinks) {
         const float sk = p.sinks[bh - (long)b * p.H] * kLog2e;
         const float m2 = fmaxf(mm, sk);
-        const float f = exp2f(mm - m2);
-        l = l * f + exp2f(sk - m2);
+        const float f = fast_exp2(mm - m2);
+        l = l * f + fast_exp2(sk - m2);
         o *= f;
       }
       store_as<QT>(p.out, bh * D + d, o / l);
@@ -526,12 +580,12 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int D) {
     mm = fmaxf(mm, sk);
   }
   float den = 0.f;
-  for (int s = s0; s <= s1; ++s) den += exp2f(lse[s] - mm);
-  if (p.sinks) den += exp2f(sk - mm);
+  for (int s = s0; s <= s1; ++s) den += fast_exp2(lse[s] - mm);
+  if (p.sinks) den += fast_exp2(sk - mm);
   const float inv = 1.f / den;
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
     float o = 0.f;
-    for (int s = s0; s <= s1; ++s) o += exp2f(lse[s] - mm) * inv * p.part[(bh * p.splits + s) * D + d];
+    for (int s = s0; s <= s1; ++s) o += fast_exp2(lse[s] - mm) * inv * p.part[(bh * p.splits + s) * D + d];
     store_as<QT>(p.out, bh * D + d, o);
   }
 }

@@ -8,6 +8,7 @@ every call runs hand-written gfx950 HIP kernels through the C ABI in
 """
 import ctypes
 import math
+import os
 
 import torch
 
@@ -16,6 +17,14 @@ from ._native import DTYPE_CODES, call, ptr
 
 
 def _splits(max_context, batch_kv):
+    """Split count and tokens per split: the library's policy, or a fixed
+    split size from DAMENDAEMON_AMD_SPLIT_TOKENS (a multiple of 64; tuning)."""
+    forced = os.environ.get('DAMENDAEMON_AMD_SPLIT_TOKENS')
+    if forced:
+        tokens = int(forced)
+        if tokens <= 0 or tokens % 64:
+            raise ValueError('DAMENDAEMON_AMD_SPLIT_TOKENS must be a positive multiple of 64')
+        return -(-int(max_context) // tokens), tokens
     tokens = ctypes.c_int(0)
     splits = _native.library().dd_decode_splits(int(max_context), int(batch_kv), ctypes.byref(tokens))
     if splits <= 0:
