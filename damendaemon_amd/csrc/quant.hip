@@ -11,9 +11,9 @@
 // rounded fp32 quotient (53 >= 2*24+2 bits), independent of the compiler's
 // fp32 division mode.
 //
-// One thread owns one group; a 256-thread block covers 256 groups, so the
-// loads of neighbouring threads are contiguous.
+// One thread owns one channel group.
 #include "common.h"
+#include "q8.h"
 
 namespace {
 
@@ -22,19 +22,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(const void *x, long group
                                                        signed char *q, unsigned short *scale) {
   const long g = (long)blockIdx.x * 256 + threadIdx.x;
   if (g >= groups) return;
-  const long base = g * group;
-  float amax = 0.f;
-  for (int i = 0; i < group; ++i) amax = fmaxf(amax, fabsf(load_as<DT>(x, base + i)));
-  const unsigned short sbits = float_to_f16_bits((float)((double)amax / 127.0));
-  const float s = half_bits_to_float(sbits);
-  const float inv = s == 0.f ? 0.f : (float)(1.0 / (double)s);
-  for (int i = 0; i < group; ++i) {
-    const float y = load_as<DT>(x, base + i) * inv;
-    float r = floorf(fabsf(y) + 0.5f);
-    r = fminf(r, 127.f);
-    q[base + i] = (signed char)(y < 0.f ? -r : r);
-  }
-  scale[g] = sbits;
+  scale[g] = q8_group<DT>(x, g * group, group, q + g * group);
 }
 
 template <int DT>

@@ -175,3 +175,48 @@ class DecodeLaunch:
 
     def merge(self):
         self._call('dd_decode_merge')
+
+
+def rope_batch(qkv, cos, sin, positions, slots, cache_k, cache_v, heads, q_norm=None, k_norm=None, eps=1e-6,
+               precise=False, page_table=None, materialize=False):
+    """Rotary embedding + K/V cache write, same contract as damendaemon/kernels.py:325-340.
+
+    qkv (T, (heads + 2*KH)*D); cos/sin (positions, RD); writes rotated keys
+    and raw values into ``cache_k``/``cache_v`` at each token's position
+    (through ``page_table`` when given) and returns the rotated queries
+    (T, heads, 1, D), or (query, key, value) with dense (T, KH, D) copies
+    when ``materialize``.
+    """
+    _, kv_heads, context, dim = cache_k.shape
+    rotary_dim = cos.shape[-1]
+    if not 0 < rotary_dim <= dim or rotary_dim % 2 or (q_norm is not None and rotary_dim != dim):
+        raise ValueError('unsupported rotary table width')
+    tokens = qkv.shape[0]
+    if (qkv.ndim != 2 or qkv.shape[1] != (heads + 2 * kv_heads) * dim or cache_v.shape != cache_k.shape
+            or positions.shape != (tokens,) or slots.shape != (tokens,) or sin.shape != cos.shape):
+        raise ValueError('incompatible rope_batch shapes')
+    _native.require_device(qkv, cos, sin, positions, slots, cache_k, cache_v, q_norm, k_norm, page_table)
+    qkv, cos, sin = qkv.contiguous(), cos.contiguous(), sin.contiguous()
+    if not cache_k.is_contiguous() or not cache_v.is_contiguous():
+        raise ValueError('rope_batch writes contiguous caches only')
+    norm = q_norm if q_norm is not None else k_norm
+    if (q_norm is None) != (k_norm is None):
+        raise ValueError('q_norm and k_norm go together')
+    if norm is not None and (q_norm.dtype != k_norm.dtype or q_norm.numel() != dim or k_norm.numel() != dim):
+        raise ValueError('norm weights must be (dim,) of one dtype')
+    positions = positions.to(torch.int64)
+    slots = slots.to(torch.int64)
+    if page_table is not None and (page_table.dtype != torch.int32 or not page_table.is_contiguous()):
+        raise ValueError('page table must be a contiguous int32 matrix')
+    query = torch.empty((tokens, heads, 1, dim), device=qkv.device, dtype=qkv.dtype)
+    key = torch.empty((tokens, kv_heads, dim), device=qkv.device, dtype=cache_k.dtype) if materialize else None
+    value = torch.empty_like(key) if materialize else None
+    call('dd_rope_batch', ptr(qkv), DTYPE_CODES[qkv.dtype], ptr(cos), ptr(sin), DTYPE_CODES[cos.dtype], rotary_dim,
+         ptr(positions), ptr(slots), tokens, heads, kv_heads, dim,
+         ptr(None if norm is None else q_norm.contiguous()), ptr(None if norm is None else k_norm.contiguous()),
+         DTYPE_CODES[norm.dtype] if norm is not None else 0, float(eps), int(bool(precise)),
+         ptr(page_table), 0 if page_table is None else page_table.shape[0],
+         0 if page_table is None else page_table.shape[1],
+         ptr(query), ptr(cache_k), ptr(cache_v), DTYPE_CODES[cache_k.dtype], cache_k.shape[0], context,
+         ptr(key), ptr(value), _native.stream_of(qkv))
+    return (query, key, value) if materialize else query

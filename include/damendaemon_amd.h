@@ -137,6 +137,83 @@ int dd_quantize_q8(const void *x, int x_dtype, int64_t rows, int dim,
 int dd_dequantize_q8(const void *q, const void *scale, int64_t rows, int dim,
                      int group, void *out, int out_dtype, void *stream);
 
+/*
+ * Ragged-batch packer (replaces the host list comprehensions of
+ * damendaemon/paged.py:149-159 / batch.py:133-136, the segment ends of
+ * paged.py:118-120 and the slot computation of kernels.py:279-281).
+ * Inputs, int64 (n,): lengths, starts (tokens already cached), slots.
+ * Outputs (bit-exact with the reference's Python arithmetic):
+ *   cu_seqlens int64 (n+1), ends int64 (n) = cu_seqlens[1:]-1,
+ *   context_lens int64 (n) = starts+lengths,
+ *   positions/slot_ids int64 (total_tokens),
+ *   slot_map int64 (total_tokens) = table[slot, pos/P]*P + pos%P (optional),
+ *   cu_pages int32 (n+1) and gather_pages int32 (total_pages): the physical
+ *   pages of each segment's whole history in logical order (optional).
+ * total_tokens = sum(lengths) and total_pages = sum(ceil(context/P)) are
+ * given by the caller (they size the outputs).
+ */
+int dd_pack_batch(const int64_t *lengths, const int64_t *starts,
+                  const int64_t *slots, int n, int64_t total_tokens,
+                  int64_t total_pages, const int32_t *page_table,
+                  int table_rows, int table_width, int page_size,
+                  int64_t *cu_seqlens, int64_t *ends, int64_t *context_lens,
+                  int64_t *positions, int64_t *slot_ids, int64_t *slot_map,
+                  int32_t *cu_pages, int32_t *gather_pages, void *stream);
+
+/*
+ * Write new K/V rows (tokens, kv_heads, dim) into their page slots
+ * (slot_map from dd_pack_batch; negative entries are skipped): the page
+ * write half of damendaemon/kernels.py:312-319 without the rotation.
+ * elem_bytes is the cache element size (K/V already in the cache dtype).
+ */
+int dd_store_kv_pages(const void *key, const void *value, int elem_bytes,
+                      const int64_t *slot_map, int64_t tokens, int kv_heads,
+                      int dim, int page_size, int64_t capacity, void *cache_k,
+                      void *cache_v, void *stream);
+
+/*
+ * Same, quantising each (token, KV head, group) row to Q8_0 on the way into
+ * int8 pages with fp16 scale rows (..., page, dim/group).  No reference
+ * counterpart: the reference's Q8_0 cache (kv_quant.py:79-107) is dense.
+ */
+int dd_store_kv_pages_q8(const void *key, const void *value, int dtype,
+                         const int64_t *slot_map, int64_t tokens,
+                         int kv_heads, int dim, int group, int page_size,
+                         int64_t capacity, void *cache_k, void *cache_v,
+                         void *k_scale, void *v_scale, void *stream);
+
+/*
+ * Page gather (restore=0) or restore (restore=1) of one slot's first
+ * `tokens` tokens between a paged layer (2, capacity, heads, page, dim) and
+ * a dense (2, heads, tokens, dim) snapshot; replaces `_copy` of
+ * damendaemon/paged_kernels.py:8-47.  Page tails are never touched.
+ */
+int dd_copy_pages(void *cache, const int32_t *table, int table_rows,
+                  int table_width, void *dense, int elem_bytes, int64_t slot,
+                  int64_t tokens, int64_t capacity, int heads, int page,
+                  int dim, int restore, void *stream);
+
+/*
+ * Rotary embedding (+ optional QK RMS norm) of a packed (tokens,
+ * (heads + 2*kv_heads)*dim) projection, writing queries to `query`
+ * (tokens, heads, 1, dim) and rotated keys / raw values into the cache at
+ * each token's position; replaces `_rope_batch` of
+ * damendaemon/kernels.py:271-340.  page_table NULL = slotted cache of
+ * context `cache_len`; otherwise cache_len is the page size.  key_out /
+ * value_out (tokens, kv_heads, dim), optional, receive the dense copies of
+ * the `materialize` path.
+ */
+int dd_rope_batch(const void *qkv, int qkv_dtype, const void *cos,
+                  const void *sin, int cos_dtype, int rotary_dim,
+                  const int64_t *positions, const int64_t *slots,
+                  int64_t tokens, int heads, int kv_heads, int dim,
+                  const void *q_norm, const void *k_norm, int norm_dtype,
+                  float eps, int precise, const int32_t *page_table,
+                  int table_rows, int table_width, void *query, void *cache_k,
+                  void *cache_v, int cache_dtype, int64_t capacity,
+                  int cache_len, void *key_out, void *value_out,
+                  void *stream);
+
 #ifdef __cplusplus
 }
 #endif

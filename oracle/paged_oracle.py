@@ -175,6 +175,108 @@ def decode_attention_sdpa(query, cache_k, cache_v, positions, slots, page_table)
 
 
 # ---------------------------------------------------------------------------
+# a4: host packer (damendaemon/paged.py:149-159, 118-120; batch.py:133-140)
+
+def pack_batch(lengths, starts, slots, table=None, page=16):
+    """Pure-Python restatement of the reference's packing.
+
+    positions = concat(range(start_i, start_i + len_i)) (paged.py:158);
+    slot_ids = slot_i repeated len_i times (paged.py:159);
+    ends = accumulate(lengths) - 1 (paged.py:118-120);
+    cu_seqlens = [0] + accumulate(lengths);
+    slot_map[t] = table[slot, pos // page] * page + pos % page, the physical
+    row `_rope_batch` writes (kernels.py:279-281, 315, 319);
+    gather lists = table[slot_i, :ceil((start_i+len_i)/page)] per segment.
+    """
+    cu = [0]
+    for n in lengths:
+        cu.append(cu[-1] + n)
+    positions = [i for n, s in zip(lengths, starts) for i in range(s, s + n)]
+    slot_ids = [slot for slot, n in zip(slots, lengths) for _ in range(n)]
+    out = {'cu_seqlens': cu, 'ends': [e - 1 for e in cu[1:]], 'positions': positions, 'slot_ids': slot_ids,
+           'context_lens': [s + n for s, n in zip(starts, lengths)]}
+    if table is not None:
+        out['slot_map'] = [int(table[slot, pos // page]) * page + pos % page for pos, slot in zip(positions, slot_ids)]
+        cu_pages, gather = [0], []
+        for s, n, slot in zip(starts, lengths, slots):
+            count = -(-(s + n) // page)
+            gather += [int(table[slot, j]) for j in range(count)]
+            cu_pages.append(cu_pages[-1] + count)
+        out['cu_pages'] = cu_pages
+        out['gather_pages'] = gather
+    return out
+
+
+# ---------------------------------------------------------------------------
+# a5: rotary embedding + page write (damendaemon/kernels.py:271-340)
+
+def _f16(x):
+    return x.to(torch.float16).to(torch.float32)
+
+
+def rope_rows(x, cos_rows, sin_rows, weight=None, eps=1e-6, precise=False):
+    """Rotate rows x (N, D) with per-row cos/sin (N, RD), fp32 arithmetic.
+
+    Follows kernels.py:288-311: optional RMS norm (x * rsqrt(mean(x^2)+eps),
+    then * weight), fp16 rounding after each multiply unless ``precise``;
+    partner channel (j + RD/2) % RD negated for j < RD/2; channels >= RD
+    keep cos 1, sin 0; a = x*cos, b = other*sin, each rounded to fp16
+    unless ``precise``; result a + b.  Each product is its own fp32 op.
+    """
+    x = x.float()
+    N, D = x.shape
+    RD = cos_rows.shape[-1]
+    idx = [(j + RD // 2) % RD for j in range(D)]
+    other = x[:, idx]
+    if weight is not None:
+        inv = torch.rsqrt((x * x).sum(-1, keepdim=True) / D + eps)
+        w = weight.float()
+        x = x * inv
+        other = other * inv
+        if not precise:
+            x, other = _f16(x), _f16(other)
+        x = x * w
+        other = other * w[idx]
+        if not precise:
+            x, other = _f16(x), _f16(other)
+    sign = torch.ones(D)
+    sign[:RD // 2] = -1
+    other = other * sign
+    cos = torch.ones(N, D)
+    sin = torch.zeros(N, D)
+    cos[:, :RD] = cos_rows.float()
+    sin[:, :RD] = sin_rows.float()
+    a = x * cos
+    b = other * sin
+    if not precise:
+        a, b = _f16(a), _f16(b)
+    return a + b
+
+
+def rope_batch(qkv, cos, sin, positions, slots, cache_k, cache_v, heads, q_norm=None, k_norm=None, eps=1e-6,
+               precise=False, page_table=None):
+    """Returns (query (T,H,1,D), new cache_k, new cache_v, key (T,KH,D), value (T,KH,D)), CPU."""
+    T = qkv.shape[0]
+    _, KH, C, D = cache_k.shape
+    x = qkv.float().reshape(T, heads + 2 * KH, D)
+    pos = positions.long()
+    cr, sr = cos[pos], sin[pos]
+    q = torch.stack([rope_rows(x[:, h], cr, sr, q_norm, eps, precise) for h in range(heads)], 1)
+    k = torch.stack([rope_rows(x[:, heads + h], cr, sr, k_norm, eps, precise) for h in range(KH)], 1)
+    v = x[:, heads + KH:]
+    ck, cv = cache_k.clone(), cache_v.clone()
+    for t in range(T):
+        p, s = int(pos[t]), int(slots[t])
+        if page_table is not None:
+            row, off = int(page_table[s, p // C]), p % C
+        else:
+            row, off = s, p
+        ck[row, :, off] = k[t].to(ck.dtype)
+        cv[row, :, off] = v[t].to(cv.dtype)
+    return q.to(qkv.dtype).unsqueeze(2), ck, cv, k.to(cache_k.dtype), v.to(cache_k.dtype)
+
+
+# ---------------------------------------------------------------------------
 # How each function is pinned (exercised in tests/test_oracle.py).
 PINNING = {
     'gather_pages': 'brute-force page walk vs torch.cat of pages '
@@ -190,4 +292,10 @@ PINNING = {
     't5_bucket': 'brute force against the bucket table a Python float64 restatement of '
                  'kernels.py:162-167 gives at the exact/large boundary',
     'decode_attention_sdpa': 'agrees with decode_attention on random pages',
+    'pack_batch': 'hand-written known answers (tests/test_oracle.py) and invariants: '
+                  'positions step by one inside a segment, slot_map decodes to the page-table entry',
+    'rope_rows': 'precise path vs the closed form x*cos + cat(-b, a)*sin of '
+                 'scripts/verify_paged_kernels.py:40-43 (and verify_kernels.py QK-norm variant); '
+                 'rounding points: a row whose products are exact in fp16 gives identical '
+                 'precise / non-precise results, a row with an fp16 tie rounds to even',
 }

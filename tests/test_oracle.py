@@ -137,3 +137,51 @@ def test_sdpa_baseline_agrees_with_oracle():
     b = O.decode_attention_sdpa(case['query'], case['cache_k'], case['cache_v'], case['positions'], case['slots'],
                                 case['page_table'])
     assert torch.allclose(a.float(), b, atol=2e-5)
+
+
+def test_pack_known_answer():
+    table = torch.tensor([[7, 3, 9, -1], [2, 5, -1, -1], [0, 1, 4, 6]], dtype=torch.int32)
+    out = O.pack_batch([3, 1, 2], [15, 0, 33], [0, 1, 2], table, page=16)
+    assert out['cu_seqlens'] == [0, 3, 4, 6]
+    assert out['ends'] == [2, 3, 5]
+    assert out['positions'] == [15, 16, 17, 0, 33, 34]
+    assert out['slot_ids'] == [0, 0, 0, 1, 2, 2]
+    assert out['slot_map'] == [7 * 16 + 15, 3 * 16 + 0, 3 * 16 + 1, 2 * 16, 4 * 16 + 1, 4 * 16 + 2]
+    assert out['context_lens'] == [18, 1, 35]
+    assert out['cu_pages'] == [0, 2, 3, 6]
+    assert out['gather_pages'] == [7, 3, 2, 0, 1, 4]
+
+
+def test_rope_precise_matches_closed_form():
+    """scripts/verify_paged_kernels.py:40-43 and verify_kernels.py:103-110 closed forms."""
+    g = torch.Generator().manual_seed(3)
+    for D, RD in ((64, 64), (96, 96), (128, 64)):
+        x = torch.randn(5, D, generator=g)
+        ang = torch.randn(5, RD // 2, generator=g)
+        ang = torch.cat((ang, ang), -1)
+        cos, sin = ang.cos(), ang.sin()
+        got = O.rope_rows(x, cos, sin, precise=True)
+        xr = x[:, :RD]
+        a, b = xr.chunk(2, -1)
+        want = torch.cat((xr * cos + torch.cat((-b, a), -1) * sin, x[:, RD:]), -1)
+        assert torch.allclose(got, want, atol=1e-6)
+        if RD == D:
+            w = torch.randn(D, generator=g)
+            got = O.rope_rows(x, cos, sin, weight=w, precise=True)
+            xn = x * torch.rsqrt(x.square().mean(-1, keepdim=True) + 1e-6) * w
+            a, b = xn.chunk(2, -1)
+            assert torch.allclose(got, xn * cos + torch.cat((-b, a), -1) * sin, atol=1e-5)
+
+
+def test_rope_rounding_points():
+    # values whose products are exact in fp16: precise and rounded paths agree
+    x = torch.tensor([[0.5, 1.0, -2.0, 0.25]])
+    cos = torch.tensor([[1.0, 0.5, 0.5, 1.0]])
+    sin = torch.tensor([[0.5, 0.25, 0.25, 0.5]])
+    assert torch.equal(O.rope_rows(x, cos, sin), O.rope_rows(x, cos, sin, precise=True))
+    # a product on an fp16 tie: 1 + 2^-11 rounds to 1 (even) before the add
+    x = torch.tensor([[1.0 + 2 ** -11, 0.0]])
+    cos = torch.tensor([[1.0, 1.0]])
+    sin = torch.tensor([[0.0, 0.0]])
+    assert O.rope_rows(x, cos, sin)[0, 0].item() == 1.0
+    assert O.rope_rows(x, cos, sin, precise=True)[0, 0].item() == 1.0 + 2 ** -11
