@@ -28,6 +28,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBPS = 8000.0   # MI355X HBM3E, AMD datasheet
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, AMD datasheet
 
 
 def algorithmic_bytes(case, kv_bytes_per_token_head):
@@ -112,7 +113,7 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=50)
     ap.add_argument('--warmup', type=int, default=5)
-    ap.add_argument('--config', default='c2', choices=['c2', 'c3', 'c5'])
+    ap.add_argument('--config', default='c2', choices=['c2', 'c3', 'c4', 'c5'])
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--copy-probe', action='store_true',
                     help='only run 1 GiB device-to-device copies (calibrates rocprofv3 FETCH/WRITE_SIZE)')
@@ -133,6 +134,8 @@ def main():
     from damendaemon_amd import kernels
     dev = 'cuda:0'
     torch.cuda.set_device(0)
+    if args.config == 'c4':
+        return bench_mixed(args, dev)
     case, workload, dtype, nbytes = build_case(args.config, dev)
     launch = kernels.prepare_attention(case['query'], case['cache_k'], case['cache_v'], case['positions'],
                                        case['slots'], page_table=case['page_table'],
@@ -179,6 +182,61 @@ def main():
         'cpu_baseline': None if args.no_cpu_baseline else cpu_baseline(case),
     }
     print(json.dumps(line), flush=True)
+
+
+def bench_mixed(args, dev):
+    """Config C4: one step = GPU pack + K/V page write + mixed prefill/decode attention."""
+    from damendaemon_amd import kernels, packing, ragged, workloads
+    case = workloads.config_c4(device=dev)
+    table, ck, cv = case['page_table'], case['cache_k'], case['cache_v']
+    lengths, starts, slots = case['lengths'], case['starts'], case['seg_slots']
+    n_chunks = sum(1 for n in lengths if n > 1)
+    t_prefill = sum(lengths[:n_chunks])
+    flops = 4 * 32 * 128 * sum(n * s + n * (n + 1) // 2 for n, s in zip(lengths[:n_chunks], starts[:n_chunks]))
+
+    def step(ev=None):
+        packed = packing.pack_batch(lengths, starts, slots, table)
+        packing.store_kv_pages(case['k_new'], case['v_new'], packed.slot_map, ck, cv)
+        out = torch.empty_like(case['q'])
+        if ev:
+            ev[0].record()
+        ragged.prefill_attention(case['q'], ck, cv, packed, table, out=out, segments=(0, n_chunks))
+        if ev:
+            ev[1].record()
+        kernels.prepare_attention(case['q'][t_prefill:].unsqueeze(2), ck, cv, packed.positions[t_prefill:],
+                                  packed.slot_ids[t_prefill:], page_table=table,
+                                  out=out[t_prefill:].unsqueeze(2)).run()
+        if ev:
+            ev[2].record()
+        return out
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for ev in events:
+        step(ev)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    prefill_ms = statistics.mean(a.elapsed_time(b) for a, b, _ in events)
+    decode_ms = statistics.mean(b.elapsed_time(c) for _, b, c in events)
+    tflops = flops / (prefill_ms * 1e-3) / 1e12
+    ctx = [s + n for s, n in zip(starts, lengths)]
+    decode_bytes = sum(ctx[n_chunks:]) * 8 * 128 * 2 * 2
+    ms = wall / args.steps * 1e3
+    print(json.dumps({
+        'metric': 'mixed chunked-prefill + decode attention: packed tokens/s, prefill MFMA utilisation, 1 MI355X',
+        'value': sum(lengths) / (ms * 1e-3), 'unit': 'tokens/s', 'n_gpus': 1, 'steps': args.steps,
+        'warmup': args.warmup, 'ms_per_step': ms, 'higher_is_better': True, 'scaling': 'weak',
+        'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic (seeded N(0,1) Q/K/V, seeded page scatter)',
+        'config': {'workload': 'C4 mixed batch: 8 x 512-token chunks on contexts U[0,4096] + 120 decodes '
+                               'ctx U[256,8192], H32/KH8/D128, page 16 (GPU pack + page write + attention)',
+                   'prefill_kernel_ms': prefill_ms, 'decode_ms': decode_ms, 'prefill_flops': flops,
+                   'decode_hbm_gbps': decode_bytes / (decode_ms * 1e-3) / 1e9},
+        'roofline': {'bound': 'mfma', 'achieved': tflops, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
+                     'frac': tflops / PEAK_BF16_TFLOPS, 'traffic': None},
+        'cpu_baseline': None}), flush=True)
 
 
 if __name__ == '__main__':

@@ -42,6 +42,8 @@ SIGNATURES['dd_store_kv_pages_q8'] = [_p, _p, _i, _p, _i64, _i, _i, _i, _i, _i64
 SIGNATURES['dd_copy_pages'] = [_p, _p, _i, _i, _p, _i, _i64, _i64, _i64, _i, _i, _i, _i, _p]
 SIGNATURES['dd_rope_batch'] = [_p, _i, _p, _p, _i, _i, _p, _p, _i64, _i, _i, _i, _p, _p, _i, _f, _i,
                                _p, _i, _i, _p, _p, _p, _i, _i64, _i, _p, _p, _p]
+SIGNATURES['dd_prefill_attention'] = [_p, _p, _p, _i, _p, _p, _p, _i, _i, _p, _i, _i, _i, _i, _i, _i, _i64, _i,
+                                      _f, _p, _p]
 SIGNATURES['dd_decode_partials'] = SIGNATURES['dd_decode_attention']
 SIGNATURES['dd_decode_merge'] = SIGNATURES['dd_decode_attention']
 

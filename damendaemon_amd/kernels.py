@@ -72,8 +72,10 @@ def attention(query, cache_k, cache_v, positions, slots=None, window=0, scale=No
 
 def prepare_attention(query, cache_k, cache_v, positions, slots=None, window=0, scale=None, alibi=None,
                       page_table=None, relative_bias=None, relative_max_distance=128, sinks=None,
-                      *, k_scale=None, v_scale=None):
+                      *, k_scale=None, v_scale=None, out=None):
     """Validate a decode call once and return its ``DecodeLaunch``.
+
+    ``out`` (optional) is a preallocated (B, H, 1, D) contiguous output.
 
     Arguments and errors are those of ``attention`` (damendaemon/kernels.py:213-229).
     """
@@ -124,7 +126,7 @@ def prepare_attention(query, cache_k, cache_v, positions, slots=None, window=0, 
     splits, split_tokens = _splits(context, batch * kv_heads)
     return DecodeLaunch(query, cache_k, cache_v, positions, slots, page_table, kv_heads, page_size, capacity,
                         group, k_scale, v_scale, window, scale, alibi, relative_bias, buckets,
-                        relative_max_distance, sinks, splits, split_tokens)
+                        relative_max_distance, sinks, splits, split_tokens, out)
 
 
 class DecodeLaunch:
@@ -139,9 +141,11 @@ class DecodeLaunch:
 
     def __init__(self, query, cache_k, cache_v, positions, slots, page_table, kv_heads, page_size, capacity,
                  group, k_scale, v_scale, window, scale, alibi, relative_bias, buckets, relative_max_distance,
-                 sinks, splits, split_tokens):
+                 sinks, splits, split_tokens, out=None):
         batch, heads, _, dim = query.shape
-        self.out = torch.empty_like(query)
+        if out is not None and (out.shape != query.shape or out.dtype != query.dtype or not out.is_contiguous()):
+            raise ValueError('out must be a contiguous tensor shaped and typed like the query')
+        self.out = torch.empty_like(query) if out is None else out
         if splits > 1:
             self.partial = torch.empty((batch * heads, splits, dim), device=query.device, dtype=torch.float32)
             self.lse = torch.empty((batch * heads, splits), device=query.device, dtype=torch.float32)

@@ -1,0 +1,78 @@
+"""Attention over one packed continuous batch: chunked prefill + decode rows.
+
+The reference runs a prefill chunk as copy_pages (gather start+len tokens
+into a dense tensor, damendaemon/paged.py:101-104) followed by torch SDPA
+with a lower-right causal mask (qwen2.py:756-770), and decodes through
+``kernels.attention`` in a separate forward pass (scheduler.py:822-873).
+Here one packed token buffer (from ``packing.pack_batch``) is attended in
+place: multi-token segments by the paged MFMA prefill kernel, the trailing
+run of single-token segments by the split-KV decode kernel.  Both read the
+pages directly; nothing is gathered.
+"""
+import torch
+
+from . import _native, kernels
+from ._native import DTYPE_CODES, call, ptr
+
+
+def _check(query, cache_k, cache_v, page_table):
+    if query.ndim == 4:
+        query = query.reshape(query.shape[0], query.shape[1], query.shape[3])
+    T, H, D = query.shape
+    capacity, KH, page, kd = cache_k.shape
+    if (kd != D or cache_v.shape != cache_k.shape or H % KH or cache_k.dtype != query.dtype
+            or cache_v.dtype != query.dtype or query.dtype not in (torch.bfloat16, torch.float16)):
+        raise ValueError('prefill attention needs bf16/fp16 query and pages of one dtype and head size')
+    if not (query.is_contiguous() and cache_k.is_contiguous() and cache_v.is_contiguous()):
+        raise ValueError('prefill attention needs contiguous tensors')
+    if page_table.dtype != torch.int32 or page_table.ndim != 2 or not page_table.is_contiguous():
+        raise ValueError('page table must be a contiguous int32 matrix')
+    _native.require_device(query, cache_k, cache_v, page_table)
+    return query
+
+
+def prefill_attention(query, cache_k, cache_v, packed, page_table, window=0, scale=None, out=None,
+                      segments=None):
+    """Causal attention of every packed query token over its slot's pages.
+
+    query (T, H, D) or (T, H, 1, D); ``packed`` from ``pack_batch``; the
+    chunk's own K/V must already be in the pages.  ``segments`` (a, b)
+    restricts the work to segments a..b-1 (their tokens only).
+    """
+    q = _check(query, cache_k, cache_v, page_table)
+    T, H, D = q.shape
+    out = torch.empty_like(q) if out is None else out.reshape(q.shape)
+    a, b = segments if segments is not None else (0, len(packed.lengths))
+    if b <= a:
+        return out
+    max_len = max(packed.lengths[a:b])
+    call('dd_prefill_attention', ptr(q), ptr(cache_k), ptr(cache_v), DTYPE_CODES[q.dtype],
+         ptr(packed.cu_seqlens[a:]), ptr(packed.context_lens[a:]), ptr(packed._meta[2, a:]), b - a, max_len,
+         ptr(page_table), page_table.shape[0], page_table.shape[1], H, cache_k.shape[1], D, cache_k.shape[2],
+         cache_k.shape[0], int(window or 0), float(D ** -.5 if scale is None else scale), ptr(out),
+         _native.stream_of(q))
+    return out
+
+
+def ragged_attention(query, cache_k, cache_v, packed, page_table, window=0, scale=None):
+    """Mixed batch: the trailing single-token segments decode, the rest prefill.
+
+    Returns (T, H, D) in the query dtype.
+    """
+    q = _check(query, cache_k, cache_v, page_table)
+    T, H, D = q.shape
+    out = torch.empty_like(q)
+    lengths = packed.lengths
+    n = len(lengths)
+    first_decode = n
+    while first_decode > 0 and lengths[first_decode - 1] == 1:
+        first_decode -= 1
+    t_decode = sum(lengths[:first_decode])
+    if first_decode > 0:
+        prefill_attention(q, cache_k, cache_v, packed, page_table, window, scale, out, (0, first_decode))
+    if first_decode < n:
+        rows = slice(t_decode, T)
+        kernels.prepare_attention(q[rows].unsqueeze(2), cache_k, cache_v, packed.positions[rows],
+                                  packed.slot_ids[rows], window=window, scale=scale, page_table=page_table,
+                                  out=out[rows].unsqueeze(2)).run()
+    return out

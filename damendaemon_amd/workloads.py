@@ -105,3 +105,26 @@ def config_c2(device='cuda', seed=2, dtype=torch.bfloat16):
 def config_c5(device='cuda', seed=5):
     return paged_decode_case([32768] * 16, 16, 2, 256, torch.bfloat16, seed=seed, device=device,
                              capacity=16 * 32768 // PAGE, outlier_frac=0.01)
+
+
+def config_c4(device='cuda', seed=4, dtype=torch.bfloat16, chunks=8, chunk=512, decodes=120):
+    """Mixed continuous batch: ``chunks`` prefill chunks of ``chunk`` tokens appended
+    to contexts U[0,4096], then ``decodes`` single-token rows with contexts U[256,8192].
+
+    Returns the paged case (history already in the pages), plus the packed
+    segment lists and new query / K / V rows for every packed token.
+    """
+    g = torch.Generator().manual_seed(seed)
+    chunk_starts = torch.randint(0, 4097, (chunks,), generator=g).tolist()
+    decode_ctx = torch.randint(256, 8193, (decodes,), generator=g).tolist()
+    lengths = [chunk] * chunks + [1] * decodes
+    starts = chunk_starts + [c - 1 for c in decode_ctx]
+    contexts = [s + n for s, n in zip(starts, lengths)]
+    case = paged_decode_case(contexts, 32, 8, 128, dtype, seed=seed, device=device)
+    gd = _gen(device, seed + 100)
+    T = sum(lengths)
+    case.update(lengths=lengths, starts=starts, seg_slots=list(range(len(lengths))),
+                q=torch.randn((T, 32, 128), generator=gd, device=device).to(dtype),
+                k_new=torch.randn((T, 8, 128), generator=gd, device=device).to(dtype),
+                v_new=torch.randn((T, 8, 128), generator=gd, device=device).to(dtype))
+    return case

@@ -214,6 +214,26 @@ int dd_rope_batch(const void *qkv, int qkv_dtype, const void *cos,
                   int cache_len, void *key_out, void *value_out,
                   void *stream);
 
+/*
+ * Chunked-prefill attention over the paged cache (the attention half of
+ * damendaemon/paged.py:97-111: copy_pages gather + lower-right causal SDPA
+ * of qwen2.py:754-770), without materialising the gathered K/V.
+ *   q, out        (T, heads, dim) packed query / output rows, bf16 or fp16
+ *   k, v          (capacity, kv_heads, page_size, dim) pages holding every
+ *                 segment's history including the chunk itself
+ *   cu_seqlens    int64 (n+1), context_lens int64 (n) = start+len, slots int64 (n)
+ *   max_len       the longest segment (sizes the grid)
+ * Row j of segment i attends keys 0 .. start_i + j (and > that - window).
+ */
+int dd_prefill_attention(const void *q, const void *k, const void *v,
+                         int dtype, const int64_t *cu_seqlens,
+                         const int64_t *context_lens, const int64_t *slots,
+                         int n, int max_len, const int32_t *page_table,
+                         int table_rows, int table_width, int heads,
+                         int kv_heads, int dim, int page_size,
+                         int64_t capacity, int window, float scale, void *out,
+                         void *stream);
+
 #ifdef __cplusplus
 }
 #endif

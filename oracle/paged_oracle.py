@@ -277,6 +277,39 @@ def rope_batch(qkv, cos, sin, positions, slots, cache_k, cache_v, heads, q_norm=
 
 
 # ---------------------------------------------------------------------------
+# a9: chunked prefill attention (damendaemon/paged.py:97-111, qwen2.py:754-770)
+
+def prefill_attention(query, cache_k, cache_v, lengths, starts, slots, page_table, window=0, scale=None,
+                      rows=None):
+    """float64 attention of packed query rows (T, H, D) over paged history.
+
+    Segment i's row j sits at position starts[i] + j and sees keys
+    0 .. starts[i] + j of slot i (lower-right causal), and with a window
+    only keys > position - window (qwen2.py:765-770).  ``rows`` limits the
+    work to some segments (others stay NaN).
+    """
+    T, H, D = query.shape
+    KH = cache_k.shape[1]
+    G = H // KH
+    scale = D ** -.5 if scale is None else scale
+    out = torch.full((T, H, D), float('nan'), dtype=torch.float64)
+    t0 = 0
+    for i, (n, s, slot) in enumerate(zip(lengths, starts, slots)):
+        if rows is None or i in rows:
+            k = gather_pages(cache_k, page_table, slot, s + n).double()
+            v = gather_pages(cache_v, page_table, slot, s + n).double()
+            for j in range(n):
+                p = s + j
+                lo = max(0, p - window + 1) if window else 0
+                for h in range(H):
+                    logits = (k[h // G, lo:p + 1] @ query[t0 + j, h].double()) * scale
+                    w = torch.softmax(logits, 0)
+                    out[t0 + j, h] = w @ v[h // G, lo:p + 1]
+        t0 += n
+    return out
+
+
+# ---------------------------------------------------------------------------
 # How each function is pinned (exercised in tests/test_oracle.py).
 PINNING = {
     'gather_pages': 'brute-force page walk vs torch.cat of pages '
@@ -292,6 +325,7 @@ PINNING = {
     't5_bucket': 'brute force against the bucket table a Python float64 restatement of '
                  'kernels.py:162-167 gives at the exact/large boundary',
     'decode_attention_sdpa': 'agrees with decode_attention on random pages',
+    'prefill_attention': 'torch SDPA with causal_lower_right on the gathered K/V (library routine)',
     'pack_batch': 'hand-written known answers (tests/test_oracle.py) and invariants: '
                   'positions step by one inside a segment, slot_map decodes to the page-table entry',
     'rope_rows': 'precise path vs the closed form x*cos + cat(-b, a)*sin of '

@@ -185,3 +185,20 @@ def test_rope_rounding_points():
     sin = torch.tensor([[0.0, 0.0]])
     assert O.rope_rows(x, cos, sin)[0, 0].item() == 1.0
     assert O.rope_rows(x, cos, sin, precise=True)[0, 0].item() == 1.0 + 2 ** -11
+
+
+def test_prefill_oracle_matches_sdpa_lower_right():
+    from torch.nn.attention.bias import causal_lower_right
+    case = paged_decode_case([40, 100], 4, 2, 32, torch.float32, seed=11)
+    lengths, starts, slots = [7, 30], [33, 70], [0, 1]
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn(sum(lengths), 4, 32, generator=g)
+    out = O.prefill_attention(q, case['cache_k'], case['cache_v'], lengths, starts, slots, case['page_table'])
+    t0 = 0
+    for n, s, slot in zip(lengths, starts, slots):
+        k = O.gather_pages(case['cache_k'], case['page_table'], slot, s + n)[None].double()
+        v = O.gather_pages(case['cache_v'], case['page_table'], slot, s + n)[None].double()
+        qq = q[t0:t0 + n].transpose(0, 1)[None].double()
+        ref = F.scaled_dot_product_attention(qq, k, v, attn_mask=causal_lower_right(n, s + n), enable_gqa=True)
+        assert torch.allclose(out[t0:t0 + n], ref[0].transpose(0, 1), atol=1e-12)
+        t0 += n
