@@ -199,6 +199,8 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
     long cb[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) cb[j] = chunk_base(kt * 4 + j);
+    // every key of the tile live and backed by a page (workgroup-uniform)
+    const bool whole = (kt + 1) * kKeys <= context && cb[0] >= 0 && cb[1] >= 0 && cb[2] >= 0 && cb[3] >= 0;
 #pragma unroll
     for (int j = 0; j < KLOADS; ++j) {
       const int idx = tid + 256 * j;
@@ -215,9 +217,11 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
       const int ch = idx - key * KCH;
       const long base = cb[key >> 4];
       const long off = (base < 0 ? 0 : base) + (long)(key & 15) * D + 8 * ch;
-      const u32x4 x = *(const u32x4 *)(vbytes + 2 * off);
-      const bool ok = (base >= 0) & (kt * kKeys + key < context);
-      vreg[j] = ok ? x : u32x4{0, 0, 0, 0};  // dead keys must not carry NaN into P.V
+      vreg[j] = *(const u32x4 *)(vbytes + 2 * off);
+      if (!whole) {  // dead keys must not carry NaN into P.V
+        const bool ok = (base >= 0) & (kt * kKeys + key < context);
+        vreg[j] = ok ? vreg[j] : u32x4{0, 0, 0, 0};
+      }
     }
   };
 
@@ -254,48 +258,65 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
     }
     // ---- mask, online softmax per column ----
     // A tile below every column's diagonal (and inside every window) needs
-    // no mask; the test is workgroup-uniform.  Masked columns (past the
-    // segment) keep their finite logits and are never stored.
+    // no mask; the test is workgroup-uniform.  Columns past the segment keep
+    // finite logits and are never stored.  The running max is kept on raw
+    // logits (scale > 0) and the scale is folded into the exp argument.
     const int kbase = kt * kKeys;
     const bool full = kbase + kKeys - 1 <= start + r0 &&
                       (p.window == 0 || kbase >= start + r0 + rows_here - p.window);
+    const float sc = p.scale_log2;
+    bool grew = false;
+    float alpha[NQ];
 #pragma unroll
     for (int nq = 0; nq < NQ; ++nq) {
-      const int lo = p.window > 0 ? qpos[nq] - p.window + 1 : -1;
       float mx = kNegInf;
+      if (full) {
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+        for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float x = s[mt][nq][i] * p.scale_log2;
-          if (!full) {
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[mt][nq][i]);
+        }
+      } else {
+        const int lo = p.window > 0 ? qpos[nq] - p.window + 1 : -1;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
             const int key = kbase + 16 * mt + 4 * g4 + i;
             const bool ok = (key <= qpos[nq]) & (key >= lo);
-            x = ok ? x : kNegInf;
+            const float x = ok ? s[mt][nq][i] : kNegInf;
+            s[mt][nq][i] = x;
+            mx = fmaxf(mx, x);
           }
-          s[mt][nq][i] = x;
-          mx = fmaxf(mx, x);
         }
       }
       mx = fmaxf(mx, shfl(mx, lane ^ 16));
       mx = fmaxf(mx, shfl(mx, lane ^ 32));
       const float mn = fmaxf(m_run[nq], mx);
-      const float mu = mn == kNegInf ? 0.f : mn;
-      const float alpha = __builtin_amdgcn_exp2f(m_run[nq] - mu);
+      grew |= mn > m_run[nq];
+      const float mu = mn == kNegInf ? 0.f : mn * sc;
+      alpha[nq] = __builtin_amdgcn_exp2f(m_run[nq] * sc - mu);
       m_run[nq] = mn;
       float ls = 0.f;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float e = __builtin_amdgcn_exp2f(s[mt][nq][i] - mu);
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[mt][nq][i], sc, -mu));
           s[mt][nq][i] = e;
           ls += e;
         }
       }
-      l_run[nq] = l_run[nq] * alpha + ls;
+      l_run[nq] = l_run[nq] * alpha[nq] + ls;
+    }
+    // O is rescaled only when some column's running max grew in this tile
+    // (after the first tiles this is rare); the test is wave-uniform.
+    if (__builtin_amdgcn_ballot_w64(grew)) {
 #pragma unroll
-      for (int md = 0; md < MD; ++md) o[md][nq] *= alpha;
+      for (int nq = 0; nq < NQ; ++nq) {
+#pragma unroll
+        for (int md = 0; md < MD; ++md) o[md][nq] *= alpha[nq];
+      }
     }
     // ---- O^T += V^T P^T : keys contracted in the order of the S^T layout ----
     // k-slot 8*g4 + j of a 32-key chunk c2 is key 32c2 + 4g4 + j (j < 4) or
