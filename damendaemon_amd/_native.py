@@ -44,6 +44,8 @@ SIGNATURES['dd_rope_batch'] = [_p, _i, _p, _p, _i, _i, _p, _p, _i64, _i, _i, _i,
                                _p, _i, _i, _p, _p, _p, _i, _i64, _i, _p, _p, _p]
 SIGNATURES['dd_prefill_attention'] = [_p, _p, _p, _i, _p, _p, _p, _i, _i, _p, _i, _i, _i, _i, _i, _i, _i64, _i,
                                       _f, _p, _p]
+SIGNATURES['dd_prefill_indices'] = [_i64, _i, _i, _i64, _i64, _p, _p]
+SIGNATURES['dd_ring_decode_indices'] = [_p, _i64, _i, _i, _i, _p, _p]
 SIGNATURES['dd_decode_partials'] = SIGNATURES['dd_decode_attention']
 SIGNATURES['dd_decode_merge'] = SIGNATURES['dd_decode_attention']
 

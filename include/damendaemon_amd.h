@@ -234,6 +234,22 @@ int dd_prefill_attention(const void *q, const void *k, const void *v,
                          int64_t capacity, int window, float scale, void *out,
                          void *stream);
 
+/*
+ * Index plans of damendaemon/cache_indices.py:24-80 (DeepSeek-style
+ * windowed + compressed-block attention), int64, -1 = padding.
+ * dd_prefill_indices: out (query_stop - query_start, min(window, seq_len)
+ *   + (ratio ? query_stop / ratio : 0)).
+ * dd_ring_decode_indices: positions int64 (rows); out (rows, window +
+ *   compressed) with compressed = (max(positions) + 1) / ratio (0 without
+ *   a ratio), computed by the caller.
+ */
+int dd_prefill_indices(int64_t seq_len, int window, int ratio,
+                       int64_t query_start, int64_t query_stop, int64_t *out,
+                       void *stream);
+int dd_ring_decode_indices(const int64_t *positions, int64_t rows, int window,
+                           int ratio, int compressed, int64_t *out,
+                           void *stream);
+
 #ifdef __cplusplus
 }
 #endif
