@@ -42,7 +42,7 @@ SIGNATURES['dd_store_kv_pages_q8'] = [_p, _p, _i, _p, _i64, _i, _i, _i, _i, _i64
 SIGNATURES['dd_copy_pages'] = [_p, _p, _i, _i, _p, _i, _i64, _i64, _i64, _i, _i, _i, _i, _p]
 SIGNATURES['dd_rope_batch'] = [_p, _i, _p, _p, _i, _i, _p, _p, _i64, _i, _i, _i, _p, _p, _i, _f, _i,
                                _p, _i, _i, _p, _p, _p, _i, _i64, _i, _p, _p, _p]
-SIGNATURES['dd_prefill_attention'] = [_p, _p, _p, _i, _p, _p, _p, _i, _i, _p, _i, _i, _i, _i, _i, _i, _i64, _i,
+SIGNATURES['dd_prefill_attention'] = [_p, _p, _p, _i, _p, _p, _p, _i, _i, _i, _p, _i, _i, _i, _i, _i, _i, _i64, _i,
                                       _f, _p, _p]
 SIGNATURES['dd_prefill_indices'] = [_i64, _i, _i, _i64, _i64, _p, _p]
 SIGNATURES['dd_ring_decode_indices'] = [_p, _i64, _i, _i, _i, _p, _p]

@@ -26,12 +26,23 @@
 //     beyond two xor-steps.
 #include "common.h"
 
-#include <cstdlib>
+#ifndef DD_PREFILL_PIPE_S
+#define DD_PREFILL_PIPE_S 0
+#endif
+// Compute S of tile kt+1 during the softmax of tile kt (needs a second S
+// register set; only worth it when it does not push the kernel into spills).
+constexpr bool kPipeS = DD_PREFILL_PIPE_S;
+#ifndef DD_PREFILL_NW
+#define DD_PREFILL_NW 8
+#endif
+#ifndef DD_PREFILL_NQ128
+#define DD_PREFILL_NQ128 2
+#endif
 
 namespace {
 
-constexpr int kKeys = 64;       // keys per tile
 constexpr float kNegInf = -__builtin_inff();
+constexpr int kTabCache = 8192;  // page-table entries staged in LDS (128K keys at page 16)
 
 struct PrefillParams {
   const void *q;       // (T, H, D)
@@ -77,6 +88,14 @@ DD_DEV u32x2 read_tr16(const unsigned short *p) {
   return __builtin_bit_cast(u32x2, v);
 }
 
+// A wave-uniform pointer, made provably scalar (SGPR pair) for the compiler.
+DD_DEV const char *uniform_ptr(const char *p) {
+  const unsigned long long v = (unsigned long long)p;
+  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+  const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+  return (const char *)(((unsigned long long)hi << 32) | lo);
+}
+
 // Eight fp32 probabilities -> one 8 x 16-bit MFMA operand (RNE).
 template <int DT>
 DD_DEV u32x4 pack8(f32x4 x0, f32x4 x1) {
@@ -104,19 +123,38 @@ DD_DEV unsigned pack2(float a, float b) {
   }
 }
 
-template <int DT, int D, int NQ>
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
-  constexpr int NC = D / 32;         // k-chunks of q.k
-  constexpr int MD = D / 16;         // O^T row tiles
-  constexpr int KROW = D + 8;        // K row stride (elements) in LDS: 16 B pad
-  constexpr int COLS = 64 * NQ;      // (query row, head) columns per workgroup
-  constexpr int KCH = D / 8;         // 16-byte chunks per key row
-  // V row stride: 32 B of pad puts the four rows of one transposing read
-  // eight banks apart, so a 32-lane half-wave covers all 64 banks once.
-  constexpr int VROW = D + 16;
+// LDS layout of a key tile: 1 KiB blocks, each holding exactly the data one
+// wave instruction consumes, in lane order (lane l at byte 16*l or 8*l), so
+// every LDS access is lane offset + immediate and conflict-free.
+//   K block (mt, cc): lane l's 16 bytes = K[key 16mt + l%16][dims 8(l/16) + 32cc ..+8),
+//     the A operand of the S^T MFMA for key tile mt and dim chunk cc.
+//   V block pair (c2, h, mp): two 512-byte halves md = 2mp, 2mp+1; lane L of
+//     a half reads 8 bytes at 8*L: V[key 32c2 + 16h + 4(L/16) + (L%16)/4]
+//     [dims 16md + 4(L%4) ..+4) -- the addresses one transposing read wants.
+// The direct-to-LDS loads fill these blocks: DMA lane l of a V block pair
+// covers read lanes 2(l%32), 2(l%32)+1 of half l/32 (16 contiguous bytes).
+#ifndef DD_PREFILL_WAVES
+#define DD_PREFILL_WAVES 2
+#endif
 
-  __shared__ __align__(16) unsigned short s_k[kKeys * KROW];
-  __shared__ __align__(16) unsigned short s_v[kKeys * VROW];
+template <int DT, int D, int NQ, int KT, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREFILL_WAVES))) void prefill_kernel(PrefillParams p) {
+  constexpr int NC = D / 32;           // k-chunks of q.k
+  constexpr int MD = D / 16;           // O^T row tiles
+  constexpr int COLS = 16 * NQ * NW;   // (query row, head) columns per workgroup
+  constexpr int NT = 64 * NW;          // threads
+  constexpr int KBLK = (KT / 16) * NC;         // K blocks per tile
+  constexpr int VBLK = (KT / 32) * 2 * (MD / 2);  // V block pairs per tile
+  constexpr int PLANE = KBLK * 1024;
+  static_assert(KBLK == VBLK && KBLK % NW == 0, "every wave issues whole blocks");
+  constexpr int IPW = KBLK / NW;       // DMA instructions per wave per plane
+
+  // Four distinct buffers (K and V, double-buffered).  Every direct-to-LDS
+  // load and every LDS read below names one of them at compile time (the
+  // tile loop is unrolled by two), so the compiler can tell that reads of
+  // one buffer do not wait for loads still landing in another.
+  __shared__ __align__(16) char s_k0[PLANE], s_k1[PLANE], s_v0[PLANE], s_v1[PLANE];
+  __shared__ int s_tab[kTabCache];                   // page-table window of this slot
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -124,14 +162,21 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
   const int g4 = lane >> 4;
   const int l16 = lane & 15;
 
-  const int kh = blockIdx.x % p.KH;
-  const int rest = blockIdx.x / p.KH;
-  const int seg = rest % p.n;
-  const int qt = rest / p.n;
+  // XCD-aware order.  Consecutive workgroups go to the 8 XCDs round-robin,
+  // each XCD with its own L2; every query tile of one (segment, KV head)
+  // group is sent to the same XCD, back to back, so they share its K/V
+  // tiles in that L2.  Within a group the longest-running tiles go first.
+  const int xcd = blockIdx.x & 7;
+  const int j = blockIdx.x >> 3;
+  const int grp = xcd + 8 * (j / p.max_tiles);
+  if (grp >= p.n * p.KH) return;
+  const int qt = p.max_tiles - 1 - j % p.max_tiles;
+  const int seg = grp / p.KH;
+  const int kh = grp - seg * p.KH;
   const long tok0 = p.cu[seg];
   const int len = (int)(p.cu[seg + 1] - tok0);
   const int G = p.G;
-  const int rows = COLS / G;                 // query rows per workgroup
+  const int rows = COLS / G;
   const int r0 = qt * rows;
   if (r0 >= len) return;
   const int context = (int)p.ctx[seg];
@@ -139,12 +184,24 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
   const long slot = p.slots[seg];
   const int rows_here = min(rows, len - r0);
 
-  // key range of the whole tile
   const int k_hi = start + r0 + rows_here;   // exclusive
   int k_lo = 0;
   if (p.window > 0) k_lo = max(0, start + r0 - p.window + 1);
-  const int kt_first = k_lo / kKeys;
-  const int kt_last = (k_hi - 1) / kKeys;
+  const int kt_first = k_lo / KT;
+  const int kt_last = (k_hi - 1) / KT;
+
+  // The page-table entries of the whole key range are staged in LDS once, so
+  // no scalar page-table load sits on the critical path of a tile's loads.
+  const int e_first = (kt_first * KT) >> p.page_shift;
+  const int e_count = ((((kt_last + 1) * KT) - 1) >> p.page_shift) - e_first + 1;
+  {
+    const bool slot_ok = slot >= 0 && slot < p.table_rows;
+    for (int i = tid; i < e_count; i += NT) {
+      const int e = e_first + i;
+      s_tab[i] = (slot_ok && e < p.table_w && i < kTabCache) ? p.table[slot * p.table_w + e] : -1;
+    }
+  }
+  __syncthreads();
 
   // ---- per-lane query columns and Q^T operands ----
   int qpos[NQ];
@@ -175,94 +232,134 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
     for (int md = 0; md < MD; ++md) o[md][nq] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // ---- global -> register staging of one key tile ----
-  // K and V: 64 keys x KCH 16-byte chunks; thread t takes chunks t, t+256, ...
-  constexpr int KLOADS = kKeys * KCH / 256;
-  u32x4 kreg[KLOADS];
-  u32x4 vreg[KLOADS];
   const char *kbytes = (const char *)p.k;
   const char *vbytes = (const char *)p.v;
-  // Element offset of the first row of 16-key chunk `ci` of this slot and KV
-  // head (page sizes are powers of two >= 16), or -1 when the chunk is not
-  // backed by an allocated page.  All arguments are workgroup-uniform, so
-  // the page-table reads are scalar loads.
+  // Element offset of the first row of 16-key chunk `ci`, or -1 when the
+  // chunk is past the context or not backed by an allocated page.
   auto chunk_base = [&](int ci) -> long {
     const int key0 = ci * 16;
     if (key0 >= context) return -1;
     const int entry = key0 >> p.page_shift;
-    if (slot < 0 || slot >= p.table_rows || entry >= p.table_w) return -1;
-    const long phys = p.table[slot * p.table_w + entry];
+    // contexts longer than kTabCache pages are rejected by the host
+    const long phys = entry - e_first < kTabCache ? uniform(s_tab[entry - e_first]) : -1;
     if (phys < 0 || phys >= p.capacity) return -1;
-    return ((phys * p.KH + kh) << p.page_shift | (key0 & (p.page - 1))) * (long)D;
+    return (((phys * p.KH + kh) << p.page_shift) | (key0 & (p.page - 1))) * (long)D;
   };
-  auto load_tile = [&](int kt) {
-    long cb[4];
+  // every key of tile kt live and backed by a page
+  auto whole = [&](int kt) {
+    if ((kt + 1) * KT > context) return false;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) cb[j] = chunk_base(kt * 4 + j);
-    // every key of the tile live and backed by a page (workgroup-uniform)
-    const bool whole = (kt + 1) * kKeys <= context && cb[0] >= 0 && cb[1] >= 0 && cb[2] >= 0 && cb[3] >= 0;
+    for (int j = 0; j < KT / 16; ++j) {
+      if (chunk_base(kt * (KT / 16) + j) < 0) return false;
+    }
+    return true;
+  };
+  // Loop-invariant per-lane byte offsets inside a 16-key chunk; each load
+  // address is a wave-uniform chunk base (SGPRs) plus one of these, so no
+  // 64-bit per-lane address has to stay live (or spill) across the loop.
+  const unsigned k_lane = 2u * (l16 * D + 8 * g4);             // K block, + 64cc bytes
+  const int vq = lane & 31;                                     // V: read-lane pair
+  const int v_key = 4 * (vq >> 3) + ((vq & 7) >> 1);           // key within the 16-key half
+  const unsigned v_lane = 2u * (v_key * D + 16 * (lane >> 5) + 8 * (vq & 1));  // + 64mp bytes
+  auto issue_k = [&](int kt, char *buf) {
 #pragma unroll
-    for (int j = 0; j < KLOADS; ++j) {
-      const int idx = tid + 256 * j;
-      const int key = idx / KCH;          // 0..63
-      const int ch = idx - key * KCH;
-      const long base = cb[key >> 4];
-      const long off = (base < 0 ? 0 : base) + (long)(key & 15) * D + 8 * ch;
-      kreg[j] = *(const u32x4 *)(kbytes + 2 * off);
+    for (int j = 0; j < IPW; ++j) {
+      const int blk = w * IPW + j;                 // K block (mt, cc)
+      const int mt = blk / NC, cc = blk - mt * NC;
+      const long kb = chunk_base(kt * (KT / 16) + mt);
+      const char *src = uniform_ptr(kbytes + 2 * ((kb < 0 ? 0 : kb) + 32 * cc)) + k_lane;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                       (__attribute__((address_space(3))) void *)(buf + blk * 1024), 16,
+                                       0, 0);
+    }
+  };
+  auto issue_v = [&](int kt, char *buf) {
+#pragma unroll
+    for (int j = 0; j < IPW; ++j) {
+      const int blk = w * IPW + j;                 // V block pair (c2, h, mp), hc = 2*c2 + h
+      const int hc = blk / (MD / 2), mp = blk - hc * (MD / 2);
+      const long vb = chunk_base(kt * (KT / 16) + hc);
+      const char *src = uniform_ptr(vbytes + 2 * ((vb < 0 ? 0 : vb) + 32 * mp)) + v_lane;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                       (__attribute__((address_space(3))) void *)(buf + blk * 1024), 16,
+                                       0, 0);
+    }
+  };
+  // Dead keys of a partial tile: zero their V bytes so 0 * garbage cannot
+  // reach the P.V product (their logits are masked to -inf as well).
+  auto zero_dead = [&](int kt, char *vbuf) {
+    for (int i = tid; i < VBLK * 64; i += NT) {
+      const int blk = i >> 6, l = i & 63;
+      const int hc = blk / (MD / 2);
+      const int q = l & 31;
+      const int key = kt * KT + 16 * hc + 4 * (q >> 3) + ((q & 7) >> 1);
+      if (key >= context || chunk_base(key >> 4) < 0)
+        *(u32x4 *)(vbuf + blk * 1024 + 16 * l) = u32x4{0, 0, 0, 0};
+    }
+  };
+  auto tile_ready = [&]() {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  };
+
+  // S^T = K Q^T for tile kt: lane holds keys 16mt + 4g4 + i for column l16.
+  // Dim chunk outer, key tile inner: consecutive MFMAs accumulate into
+  // different registers, and the K operands of chunk cc+1 are read from LDS
+  // while the MFMAs of chunk cc run.
+  auto compute_s = [&](const char *kt_lds, f32x4 (&sv)[KT / 16][NQ]) {
+    constexpr int MT = KT / 16;
+    u32x4 a[MT], an[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      a[mt] = *(const u32x4 *)(kt_lds + (mt * NC + 0) * 1024 + 16 * lane);
+#pragma unroll
+      for (int nq = 0; nq < NQ; ++nq) sv[mt][nq] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
-    for (int j = 0; j < KLOADS; ++j) {
-      const int idx = tid + 256 * j;
-      const int key = idx / KCH;
-      const int ch = idx - key * KCH;
-      const long base = cb[key >> 4];
-      const long off = (base < 0 ? 0 : base) + (long)(key & 15) * D + 8 * ch;
-      vreg[j] = *(const u32x4 *)(vbytes + 2 * off);
-      if (!whole) {  // dead keys must not carry NaN into P.V
-        const bool ok = (base >= 0) & (kt * kKeys + key < context);
-        vreg[j] = ok ? vreg[j] : u32x4{0, 0, 0, 0};
+    for (int cc = 0; cc < NC; ++cc) {
+      if (cc + 1 < NC) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) an[mt] = *(const u32x4 *)(kt_lds + (mt * NC + cc + 1) * 1024 + 16 * lane);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int nq = 0; nq < NQ; ++nq) sv[mt][nq] = mfma<DT>(a[mt], qb[nq][cc], sv[mt][nq]);
+      }
+      if (cc + 1 < NC) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) a[mt] = an[mt];
       }
     }
   };
 
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int j = 0; j < KLOADS; ++j) {
-      const int idx = tid + 256 * j;
-      const int key = idx / KCH;
-      const int ch = idx - key * KCH;
-      *(u32x4 *)(s_k + key * KROW + 8 * ch) = kreg[j];
-      *(u32x4 *)(s_v + key * VROW + 8 * ch) = vreg[j];
-    }
-  };
-
-  if (kt_first <= kt_last) load_tile(kt_first);
-  for (int kt = kt_first; kt <= kt_last; ++kt) {
-    __syncthreads();
-    store_tile();
-    __syncthreads();
-    if (kt + 1 <= kt_last) load_tile(kt + 1);
-
-    // ---- S^T = K Q^T : lane holds keys 16mt + 4g4 + i for column l16 ----
-    f32x4 s[4][NQ];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-      for (int nq = 0; nq < NQ; ++nq) s[mt][nq] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int cc = 0; cc < NC; ++cc) {
-        const u32x4 a = *(const u32x4 *)(s_k + (16 * mt + l16) * KROW + 8 * g4 + 32 * cc);
-#pragma unroll
-        for (int nq = 0; nq < NQ; ++nq) s[mt][nq] = mfma<DT>(a, qb[nq][cc], s[mt][nq]);
+  f32x4 s_a[KT / 16][NQ], s_b[KT / 16][NQ];
+  // One pipelined step for tile kt.  kc / vc: LDS buffers of K(kt) / V(kt);
+  // kn / vn: the other pair (K(kt+1) already there, V(kt+1) to be loaded).
+  auto step = [&](int kt, char *kc, char *vc, char *kn, char *vn, f32x4 (&s)[KT / 16][NQ],
+                  f32x4 (&s_next)[KT / 16][NQ]) {
+    if constexpr (kPipeS) {
+      if (kt + 2 <= kt_last) issue_k(kt + 2, kc);
+      if (kt + 1 <= kt_last) {
+        issue_v(kt + 1, vn);
+        compute_s(kn, s_next);
       }
+    } else {
+      if (kt + 1 <= kt_last) {
+        issue_k(kt + 1, kn);
+        issue_v(kt + 1, vn);
+      }
+      compute_s(kc, s);
     }
+    const char *vt_lds = vc;
+
     // ---- mask, online softmax per column ----
     // A tile below every column's diagonal (and inside every window) needs
     // no mask; the test is workgroup-uniform.  Columns past the segment keep
     // finite logits and are never stored.  The running max is kept on raw
     // logits (scale > 0) and the scale is folded into the exp argument.
-    const int kbase = kt * kKeys;
-    const bool full = kbase + kKeys - 1 <= start + r0 &&
+    const int kbase = kt * KT;
+    const bool full = kbase + KT - 1 <= start + r0 &&
                       (p.window == 0 || kbase >= start + r0 + rows_here - p.window);
     const float sc = p.scale_log2;
     bool grew = false;
@@ -272,14 +369,14 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
       float mx = kNegInf;
       if (full) {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+        for (int mt = 0; mt < KT / 16; ++mt) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[mt][nq][i]);
         }
       } else {
         const int lo = p.window > 0 ? qpos[nq] - p.window + 1 : -1;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+        for (int mt = 0; mt < KT / 16; ++mt) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int key = kbase + 16 * mt + 4 * g4 + i;
@@ -299,7 +396,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
       m_run[nq] = mn;
       float ls = 0.f;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < KT / 16; ++mt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[mt][nq][i], sc, -mu));
@@ -318,27 +415,67 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
         for (int md = 0; md < MD; ++md) o[md][nq] *= alpha[nq];
       }
     }
+
     // ---- O^T += V^T P^T : keys contracted in the order of the S^T layout ----
     // k-slot 8*g4 + j of a 32-key chunk c2 is key 32c2 + 4g4 + j (j < 4) or
     // 32c2 + 16 + 4g4 + (j - 4): exactly the keys this lane's S^T registers
     // of tiles 2c2 and 2c2+1 hold, and the keys the two transposing reads
     // below return for rows 32c2 + 4g4 + (l16/4) and 16 further on.
+    u32x4 pb[KT / 32][NQ];
 #pragma unroll
-    for (int c2 = 0; c2 < 2; ++c2) {
-      u32x4 pb[NQ];
+    for (int c2 = 0; c2 < KT / 32; ++c2) {
 #pragma unroll
-      for (int nq = 0; nq < NQ; ++nq) pb[nq] = pack8<DT>(s[2 * c2][nq], s[2 * c2 + 1][nq]);
-      const int vrow = 32 * c2 + 4 * g4 + (l16 >> 2);
+      for (int nq = 0; nq < NQ; ++nq) pb[c2][nq] = pack8<DT>(s[2 * c2][nq], s[2 * c2 + 1][nq]);
+    }
+    // V^T operand of (md, c2): half h of key chunk c2 lives in block pair
+    // (2c2 + h, md/2); the operand of the next md is read while the MFMAs of
+    // this one run.
+    auto vop = [&](int md, int c2) {
+      const char *blk0 = vt_lds + ((2 * c2) * (MD / 2) + md / 2) * 1024 + (md & 1) * 512 + 8 * lane;
+      const u32x2 lo = read_tr16((const unsigned short *)blk0);
+      const u32x2 hi = read_tr16((const unsigned short *)(blk0 + (MD / 2) * 1024));
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    };
+    u32x4 va[KT / 32], vnx[KT / 32];
 #pragma unroll
-      for (int md = 0; md < MD; ++md) {
-        const unsigned short *at = s_v + vrow * VROW + 16 * md + 4 * (l16 & 3);
-        const u32x2 lo = read_tr16(at);
-        const u32x2 hi = read_tr16(at + 16 * VROW);
-        const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
+    for (int c2 = 0; c2 < KT / 32; ++c2) va[c2] = vop(0, c2);
 #pragma unroll
-        for (int nq = 0; nq < NQ; ++nq) o[md][nq] = mfma<DT>(a, pb[nq], o[md][nq]);
+    for (int md = 0; md < MD; ++md) {
+      if (md + 1 < MD) {
+#pragma unroll
+        for (int c2 = 0; c2 < KT / 32; ++c2) vnx[c2] = vop(md + 1, c2);
+      }
+#pragma unroll
+      for (int c2 = 0; c2 < KT / 32; ++c2) {
+#pragma unroll
+        for (int nq = 0; nq < NQ; ++nq) o[md][nq] = mfma<DT>(va[c2], pb[c2][nq], o[md][nq]);
+      }
+      if (md + 1 < MD) {
+#pragma unroll
+        for (int c2 = 0; c2 < KT / 32; ++c2) va[c2] = vnx[c2];
       }
     }
+    if (kt < kt_last) {
+      tile_ready();  // K(kt+2) and V(kt+1) landed; every wave is done with kt
+      if (!whole(kt + 1)) {
+        zero_dead(kt + 1, vn);
+        __syncthreads();
+      }
+    }
+  };
+
+  issue_k(kt_first, s_k0);
+  if (kPipeS && kt_first < kt_last) issue_k(kt_first + 1, s_k1);
+  issue_v(kt_first, s_v0);
+  tile_ready();
+  if (!whole(kt_first)) {
+    zero_dead(kt_first, s_v0);
+    __syncthreads();
+  }
+  if constexpr (kPipeS) compute_s(s_k0, s_a);
+  for (int kt = kt_first; kt <= kt_last; kt += 2) {
+    step(kt, s_k0, s_v0, s_k1, s_v1, s_a, s_b);
+    if (kt + 1 <= kt_last) step(kt + 1, s_k1, s_v1, s_k0, s_v0, s_b, s_a);
   }
 
   // ---- normalise and store: lane holds dims 16md + 4g4 + i of its column ----
@@ -363,29 +500,24 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
   }
 }
 
-template <int DT, int D, int NQ>
-int launch(const PrefillParams &p, hipStream_t s) {
-  const long grid = (long)p.max_tiles * p.n * p.KH;
+template <int DT, int D, int NQ, int KT, int NW>
+int launch(PrefillParams p, int max_len, hipStream_t s) {
+  if (16 * NQ * NW / p.G < 1) return DD_EUNSUPPORTED;
+  p.max_tiles = (int)dd_cdiv(max_len, (16 * NQ * NW) / p.G);
+  const long grid = 8L * dd_cdiv((long)p.n * p.KH, 8) * p.max_tiles;
   if (grid == 0) return DD_OK;
-  if (grid > 0x7fffffffL || 64 * NQ / p.G < 1) return DD_EUNSUPPORTED;
-  hipLaunchKernelGGL((prefill_kernel<DT, D, NQ>), dim3((unsigned)grid), dim3(256), 0, s, p);
+  if (grid > 0x7fffffffL) return DD_EUNSUPPORTED;
+  hipLaunchKernelGGL((prefill_kernel<DT, D, NQ, KT, NW>), dim3((unsigned)grid), dim3(64 * NW), 0, s, p);
   DD_LAUNCH_CHECK();
   return DD_OK;
 }
 
 template <int DT>
-int dispatch(PrefillParams p, int D, int max_len, hipStream_t s) {
-  auto tiles = [&](int nq) { return (int)dd_cdiv(max_len, (64 * nq) / p.G); };
+int dispatch(const PrefillParams &p, int D, int max_len, hipStream_t s) {
   switch (D) {
-    case 64: p.max_tiles = tiles(2); return launch<DT, 64, 2>(p, s);
-    case 128:
-      if (getenv("DAMENDAEMON_AMD_PREFILL_NQ") && atoi(getenv("DAMENDAEMON_AMD_PREFILL_NQ")) == 1) {
-        p.max_tiles = tiles(1);
-        return launch<DT, 128, 1>(p, s);
-      }
-      p.max_tiles = tiles(2);
-      return launch<DT, 128, 2>(p, s);
-    case 256: p.max_tiles = tiles(1); return launch<DT, 256, 1>(p, s);
+    case 64: return launch<DT, 64, 2, 64, DD_PREFILL_NW>(p, max_len, s);
+    case 128: return launch<DT, 128, DD_PREFILL_NQ128, 64, DD_PREFILL_NW>(p, max_len, s);
+    case 256: return launch<DT, 256, 1, 32, 4>(p, max_len, s);
     default: return DD_EUNSUPPORTED;
   }
 }
@@ -394,6 +526,7 @@ int dispatch(PrefillParams p, int D, int max_len, hipStream_t s) {
 
 extern "C" int dd_prefill_attention(const void *q, const void *k, const void *v, int dtype, const int64_t *cu_seqlens,
                                     const int64_t *context_lens, const int64_t *slots, int n, int max_len,
+                                    int max_context,
                                     const int32_t *page_table, int table_rows, int table_width, int heads,
                                     int kv_heads, int dim, int page_size, int64_t capacity, int window, float scale,
                                     void *out, void *stream) {
@@ -401,6 +534,7 @@ extern "C" int dd_prefill_attention(const void *q, const void *k, const void *v,
       heads <= 0 || kv_heads <= 0 || heads % kv_heads || page_size <= 0 || capacity <= 0 || table_width <= 0)
     return DD_EINVAL;
   if (heads / kv_heads > 16) return DD_EUNSUPPORTED;
+  if ((long)max_context > (long)kTabCache * page_size) return DD_EUNSUPPORTED;
   if (n == 0 || max_len == 0) return DD_OK;
   PrefillParams p{};
   p.q = q;

@@ -46,8 +46,11 @@ def prefill_attention(query, cache_k, cache_v, packed, page_table, window=0, sca
     if b <= a:
         return out
     max_len = max(packed.lengths[a:b])
+    max_context = max(s + n for s, n in zip(packed.starts[a:b], packed.lengths[a:b]))
+    if max_context > 8192 * cache_k.shape[2]:
+        raise ValueError('prefill attention supports up to 8192 pages of history per segment')
     call('dd_prefill_attention', ptr(q), ptr(cache_k), ptr(cache_v), DTYPE_CODES[q.dtype],
-         ptr(packed.cu_seqlens[a:]), ptr(packed.context_lens[a:]), ptr(packed._meta[2, a:]), b - a, max_len,
+         ptr(packed.cu_seqlens[a:]), ptr(packed.context_lens[a:]), ptr(packed._meta[2, a:]), b - a, max_len, max_context,
          ptr(page_table), page_table.shape[0], page_table.shape[1], H, cache_k.shape[1], D, cache_k.shape[2],
          cache_k.shape[0], int(window or 0), float(D ** -.5 if scale is None else scale), ptr(out),
          _native.stream_of(q))

@@ -223,12 +223,14 @@ int dd_rope_batch(const void *qkv, int qkv_dtype, const void *cos,
  *                 segment's history including the chunk itself
  *   cu_seqlens    int64 (n+1), context_lens int64 (n) = start+len, slots int64 (n)
  *   max_len       the longest segment (sizes the grid)
+ *   max_context   the longest start+len; at most 8192 pages per segment
  * Row j of segment i attends keys 0 .. start_i + j (and > that - window).
  */
 int dd_prefill_attention(const void *q, const void *k, const void *v,
                          int dtype, const int64_t *cu_seqlens,
                          const int64_t *context_lens, const int64_t *slots,
-                         int n, int max_len, const int32_t *page_table,
+                         int n, int max_len, int max_context,
+                         const int32_t *page_table,
                          int table_rows, int table_width, int heads,
                          int kv_heads, int dim, int page_size,
                          int64_t capacity, int window, float scale, void *out,
