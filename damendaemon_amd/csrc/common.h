@@ -113,6 +113,14 @@ DD_DEV float shfl(float x, int src_lane) {
       float, __builtin_amdgcn_ds_bpermute(src_lane << 2, __builtin_bit_cast(int, x)));
 }
 
+// A wave-uniform pointer, made provably scalar (SGPR pair) for the compiler.
+DD_DEV const char *uniform_ptr(const char *p) {
+  const unsigned long long v = (unsigned long long)p;
+  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+  const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+  return (const char *)(((unsigned long long)hi << 32) | lo);
+}
+
 // ---- host side -----------------------------------------------------------
 
 #define DD_LAUNCH_CHECK()                                   \

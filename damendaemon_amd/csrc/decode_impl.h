@@ -57,12 +57,12 @@ struct DecodeParams {
 };
 
 constexpr int kWaves = 4;
-#ifndef DD_DECODE_PREFETCH
-#define DD_DECODE_PREFETCH 0
+#ifndef DD_DECODE_PD
+#define DD_DECODE_PD 1
 #endif
-// Load the next page into a second register set while consuming the current
-// one (costs occupancy; off unless measured to win).
-constexpr bool kPrefetch = DD_DECODE_PREFETCH;
+#ifndef DD_DECODE_PD_I8
+#define DD_DECODE_PD_I8 2
+#endif
 constexpr float kNegInf = -__builtin_inff();
 
 // Element offset of the first token of 16-token chunk `pg` of (row, kh), or
@@ -162,6 +162,7 @@ __global__ __launch_bounds__(256) DD_DECODE_ATTR void decode_kernel(DecodeParams
   constexpr int NC = D / 32;                                        // MFMA k-chunks
   constexpr int NC4 = D / 16;                                       // fp32 k-chunks
   constexpr int KB = KVT == DD_F32 ? 4 : (KVT == DD_I8 ? 1 : 2);    // bytes per element
+  constexpr int PD = KVT == DD_I8 ? DD_DECODE_PD_I8 : DD_DECODE_PD;  // pages in flight per wave
 
   __shared__ float s_p[kWaves][16][GB];       // per-wave page probabilities
   __shared__ float s_o[GB][D];                // cross-wave output accumulator
@@ -286,14 +287,8 @@ __global__ __launch_bounds__(256) DD_DECODE_ATTR void decode_kernel(DecodeParams
     }
   };
 
-  PageRegs cur;
-  int pg = pg_first + w;
-  if (pg <= pg_last) load_page(pg, cur);
-  for (; pg <= pg_last; pg += kWaves) {
-    PageRegs nxt;
-    if constexpr (kPrefetch) {
-      if (pg + kWaves <= pg_last) load_page(pg + kWaves, nxt);
-    }
+  // Consume one page: logits, online softmax, p.v.
+  auto consume = [&](int pg, PageRegs &cur) {
     const long base = cur.base;
     const int t0 = pg * 16;
     const int tk = t0 + tl;
@@ -444,10 +439,25 @@ __global__ __launch_bounds__(256) DD_DECODE_ATTR void decode_kernel(DecodeParams
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if constexpr (kPrefetch) {
-      cur = nxt;
-    } else if (pg + kWaves <= pg_last) {
-      load_page(pg + kWaves, cur);
+  };
+
+  // Register ring: this wave's page i is pg_first + w + i*kWaves and lives in
+  // register set i % PD; PD pages are in flight while one is consumed.  The
+  // loop is unrolled by PD so every set has static register names.
+  const int first = pg_first + w;
+  const int n_pages = first <= pg_last ? (pg_last - first) / kWaves + 1 : 0;
+  PageRegs ring[PD];
+#pragma unroll
+  for (int u = 0; u < PD; ++u) {
+    if (u < n_pages) load_page(first + u * kWaves, ring[u]);
+  }
+  for (int i = 0; i < n_pages; i += PD) {
+#pragma unroll
+    for (int u = 0; u < PD; ++u) {
+      if (i + u < n_pages) {
+        consume(first + (i + u) * kWaves, ring[u]);
+        if (i + u + PD < n_pages) load_page(first + (i + u + PD) * kWaves, ring[u]);
+      }
     }
   }
 

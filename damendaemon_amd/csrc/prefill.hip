@@ -88,14 +88,6 @@ DD_DEV u32x2 read_tr16(const unsigned short *p) {
   return __builtin_bit_cast(u32x2, v);
 }
 
-// A wave-uniform pointer, made provably scalar (SGPR pair) for the compiler.
-DD_DEV const char *uniform_ptr(const char *p) {
-  const unsigned long long v = (unsigned long long)p;
-  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
-  const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
-  return (const char *)(((unsigned long long)hi << 32) | lo);
-}
-
 // Eight fp32 probabilities -> one 8 x 16-bit MFMA operand (RNE).
 template <int DT>
 DD_DEV u32x4 pack8(f32x4 x0, f32x4 x1) {
