@@ -16,7 +16,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 LIBRARY = Path(__file__).resolve().parent / '_lib' / 'libdamendaemon_amd.so'
 
 F32, F16, BF16, I8 = 0, 1, 2, 3
@@ -43,7 +43,8 @@ SIGNATURES['dd_copy_pages'] = [_p, _p, _i, _i, _p, _i, _i64, _i64, _i64, _i, _i,
 SIGNATURES['dd_rope_batch'] = [_p, _i, _p, _p, _i, _i, _p, _p, _i64, _i, _i, _i, _p, _p, _i, _f, _i,
                                _p, _i, _i, _p, _p, _p, _i, _i64, _i, _p, _p, _p]
 SIGNATURES['dd_prefill_attention'] = [_p, _p, _p, _i, _p, _p, _p, _i, _i, _i, _p, _i, _i, _i, _i, _i, _i, _i64, _i,
-                                      _f, _p, _p]
+                                      _f, _p, _i, _p, _p]
+SIGNATURES['dd_prefill_plan'] = [_p, _p, _i, _i, _i, _i, _i, _p, _i]
 SIGNATURES['dd_prefill_indices'] = [_i64, _i, _i, _i64, _i64, _p, _p]
 SIGNATURES['dd_ring_decode_indices'] = [_p, _i64, _i, _i, _i, _p, _p]
 SIGNATURES['dd_decode_partials'] = SIGNATURES['dd_decode_attention']

@@ -121,6 +121,32 @@ DD_DEV const char *uniform_ptr(const char *p) {
   return (const char *)(((unsigned long long)hi << 32) | lo);
 }
 
+// Reductions of x over lane pairs (l, l ^ 16) and (l, l ^ 32) with the
+// gfx950 permlane swaps (VALU, no LDS round trip).  A swap of a register
+// with itself leaves, in the two results, x of this lane and x of the
+// partner lane (in an order that depends on the lane), so the commutative
+// combination of the pair is the same in both lanes.
+DD_DEV float xor16_max(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+DD_DEV float xor32_max(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+DD_DEV float xor16_sum(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+DD_DEV float xor32_sum(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // ---- host side -----------------------------------------------------------
 
 #define DD_LAUNCH_CHECK()                                   \

@@ -26,12 +26,14 @@
 //     beyond two xor-steps.
 #include "common.h"
 
-#ifndef DD_PREFILL_PIPE_S
-#define DD_PREFILL_PIPE_S 0
-#endif
-// Compute S of tile kt+1 during the softmax of tile kt (needs a second S
-// register set; only worth it when it does not push the kernel into spills).
-constexpr bool kPipeS = DD_PREFILL_PIPE_S;
+#include <algorithm>
+#include <vector>
+
+// The running max of a column is only moved when a tile's max exceeds it by
+// more than 2^kMaxSlack in the exp2 domain: probabilities then stay <= 2^8
+// (exact in fp32 sums and bf16/f16 operands), and O and l are rescaled a few
+// times per column instead of on almost every tile.
+constexpr float kMaxSlack = 8.f;
 #ifndef DD_PREFILL_NW
 #define DD_PREFILL_NW 8
 #endif
@@ -52,6 +54,7 @@ struct PrefillParams {
   const int64_t *ctx;  // (n) start + len
   const int64_t *slots;
   const int32_t *table;
+  const int32_t *plan;  // optional: work item (group * max_tiles + qt) per workgroup, -1 = none
   void *out;           // (T, H, D)
   long capacity;
   int n, max_tiles;
@@ -125,27 +128,59 @@ DD_DEV unsigned pack2(float a, float b) {
 //     [dims 16md + 4(L%4) ..+4) -- the addresses one transposing read wants.
 // The direct-to-LDS loads fill these blocks: DMA lane l of a V block pair
 // covers read lanes 2(l%32), 2(l%32)+1 of half l/32 (16 contiguous bytes).
+//
+// Schedule.  Tile t is processed in two phases separated by workgroup
+// barriers: M(t) issues the loads of K(t+2) and V(t+1), computes S(t) =
+// K(t) Q^T and O += V(t-1)^T P(t-1)^T (all MFMA), and V(t) runs the online
+// softmax of S(t) into P(t) (all VALU).  With 8 waves the second four
+// (one per SIMD) run one barrier behind the first four, so on every SIMD
+// one wave is in an MFMA phase while the other is in a VALU phase.
+// Hazards, with both groups one phase apart: K(t) is read in M(t) and
+// V(t-1) in M(t) only, so K(t+2) may overwrite K(t-1) and V(t+1) may
+// overwrite V(t-2) once every wave has left M(t-1): three K and three V
+// buffers.  A wave issues its loads at the start of M(t) and, before each
+// barrier, waits for all of its loads except the ones issued in the current
+// M phase, which gives K(t) and V(t-1) two to four phases to land before
+// the first wave reads them.
+// Keys past the context and chunks without an allocated page are loaded as
+// zeros: every chunk load goes through a buffer resource whose size covers
+// only the chunk's live rows (out-of-range buffer loads return 0).
+
 #ifndef DD_PREFILL_WAVES
 #define DD_PREFILL_WAVES 2
 #endif
+
+// 32-bit word 3 of a raw (untyped) buffer resource.
+constexpr int kBufferWord3 = 0x00020000;
+
+typedef __attribute__((address_space(3))) void lds_void;
 
 template <int DT, int D, int NQ, int KT, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREFILL_WAVES))) void prefill_kernel(PrefillParams p) {
   constexpr int NC = D / 32;           // k-chunks of q.k
   constexpr int MD = D / 16;           // O^T row tiles
+  constexpr int MT = KT / 16;          // 16-key chunks per tile
+  constexpr int C2 = KT / 32;          // 32-key MFMA k-steps of P.V per tile
   constexpr int COLS = 16 * NQ * NW;   // (query row, head) columns per workgroup
   constexpr int NT = 64 * NW;          // threads
-  constexpr int KBLK = (KT / 16) * NC;         // K blocks per tile
-  constexpr int VBLK = (KT / 32) * 2 * (MD / 2);  // V block pairs per tile
+  constexpr int KBLK = MT * NC;        // K blocks per tile
+  constexpr int VBLK = C2 * 2 * (MD / 2);  // V block pairs per tile
   constexpr int PLANE = KBLK * 1024;
   static_assert(KBLK == VBLK && KBLK % NW == 0, "every wave issues whole blocks");
   constexpr int IPW = KBLK / NW;       // DMA instructions per wave per plane
+  static_assert(NC % IPW == 0 && MD / 2 == NC, "a wave's blocks share one 16-key chunk");
+  static_assert(2 * IPW < 16, "vmcnt immediate");
+#ifndef DD_PREFILL_PINGPONG
+#define DD_PREFILL_PINGPONG 0
+#endif
+  constexpr bool kPingPong = DD_PREFILL_PINGPONG && NW == 8;  // waves w and w+4 share a SIMD
 
-  // Four distinct buffers (K and V, double-buffered).  Every direct-to-LDS
-  // load and every LDS read below names one of them at compile time (the
-  // tile loop is unrolled by two), so the compiler can tell that reads of
-  // one buffer do not wait for loads still landing in another.
-  __shared__ __align__(16) char s_k0[PLANE], s_k1[PLANE], s_v0[PLANE], s_v1[PLANE];
+  // Six distinct buffers (three K, three V).  Every direct-to-LDS load and
+  // every LDS read below names one of them at compile time (the tile loop is
+  // unrolled by three), so the compiler can tell that reads of one buffer do
+  // not wait for loads still landing in another.
+  __shared__ __align__(1024) char s_v0[PLANE], s_v1[PLANE], s_v2[PLANE];  // lowest addresses: read most
+  __shared__ __align__(16) char s_k0[PLANE], s_k1[PLANE], s_k2[PLANE];
   __shared__ int s_tab[kTabCache];                   // page-table window of this slot
 
   const int tid = threadIdx.x;
@@ -154,15 +189,23 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREF
   const int g4 = lane >> 4;
   const int l16 = lane & 15;
 
-  // XCD-aware order.  Consecutive workgroups go to the 8 XCDs round-robin,
+  // Without a plan: consecutive workgroups go to the 8 XCDs round-robin,
   // each XCD with its own L2; every query tile of one (segment, KV head)
-  // group is sent to the same XCD, back to back, so they share its K/V
-  // tiles in that L2.  Within a group the longest-running tiles go first.
-  const int xcd = blockIdx.x & 7;
-  const int j = blockIdx.x >> 3;
-  const int grp = xcd + 8 * (j / p.max_tiles);
+  // group is sent to the same XCD, longest first.  With a plan
+  // (dd_prefill_plan) the host has chosen and balanced this order.
+  int grp, qt;
+  if (p.plan) {
+    const int item = p.plan[blockIdx.x];
+    if (item < 0) return;
+    grp = item / p.max_tiles;
+    qt = item - grp * p.max_tiles;
+  } else {
+    const int xcd = blockIdx.x & 7;
+    const int j = blockIdx.x >> 3;
+    grp = xcd + 8 * (j / p.max_tiles);
+    qt = p.max_tiles - 1 - j % p.max_tiles;
+  }
   if (grp >= p.n * p.KH) return;
-  const int qt = p.max_tiles - 1 - j % p.max_tiles;
   const int seg = grp / p.KH;
   const int kh = grp - seg * p.KH;
   const long tok0 = p.cu[seg];
@@ -182,18 +225,19 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREF
   const int kt_first = k_lo / KT;
   const int kt_last = (k_hi - 1) / KT;
 
-  // The page-table entries of the whole key range are staged in LDS once, so
-  // no scalar page-table load sits on the critical path of a tile's loads.
+  // The page-table entries of the whole key range are staged in LDS once,
+  // already validated (-1 for an unallocated entry or one outside the cache),
+  // so no global page-table load or bounds test sits on a tile's critical path.
   const int e_first = (kt_first * KT) >> p.page_shift;
   const int e_count = ((((kt_last + 1) * KT) - 1) >> p.page_shift) - e_first + 1;
   {
     const bool slot_ok = slot >= 0 && slot < p.table_rows;
-    for (int i = tid; i < e_count; i += NT) {
+    for (int i = tid; i < e_count && i < kTabCache; i += NT) {
       const int e = e_first + i;
-      s_tab[i] = (slot_ok && e < p.table_w && i < kTabCache) ? p.table[slot * p.table_w + e] : -1;
+      const int phys = (slot_ok && e < p.table_w) ? p.table[slot * p.table_w + e] : -1;
+      s_tab[i] = (phys >= 0 && phys < p.capacity) ? phys : -1;
     }
   }
-  __syncthreads();
 
   // ---- per-lane query columns and Q^T operands ----
   int qpos[NQ];
@@ -215,97 +259,92 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREF
   }
 
   f32x4 o[MD][NQ];
-  float m_run[NQ], l_run[NQ];
+  float m_run[NQ], l_run[NQ], alpha[NQ];
+  bool grew = false;
 #pragma unroll
   for (int nq = 0; nq < NQ; ++nq) {
     m_run[nq] = kNegInf;
     l_run[nq] = 0.f;
+    alpha[nq] = 1.f;
 #pragma unroll
     for (int md = 0; md < MD; ++md) o[md][nq] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  __syncthreads();  // s_tab
 
-  const char *kbytes = (const char *)p.k;
-  const char *vbytes = (const char *)p.v;
-  // Element offset of the first row of 16-key chunk `ci`, or -1 when the
-  // chunk is past the context or not backed by an allocated page.
-  auto chunk_base = [&](int ci) -> long {
-    const int key0 = ci * 16;
-    if (key0 >= context) return -1;
-    const int entry = key0 >> p.page_shift;
-    // contexts longer than kTabCache pages are rejected by the host
-    const long phys = entry - e_first < kTabCache ? uniform(s_tab[entry - e_first]) : -1;
-    if (phys < 0 || phys >= p.capacity) return -1;
-    return (((phys * p.KH + kh) << p.page_shift) | (key0 & (p.page - 1))) * (long)D;
+  // ---- loads ----
+  // A window of 64 consecutive staged page-table entries, one per lane, that
+  // starts at the first entry of tile kt; it covers tiles kt and kt+1 (a tile
+  // spans at most KT/16 <= 4 entries), so a tile's entries are read with
+  // v_readlane instead of a dependent LDS round trip each.
+  auto read_window = [&](int kt) -> int {
+    const int i = ((kt * KT) >> p.page_shift) - e_first + lane;
+    return s_tab[i < kTabCache ? i : kTabCache - 1];
   };
-  // every key of tile kt live and backed by a page
-  auto whole = [&](int kt) {
-    if ((kt + 1) * KT > context) return false;
-#pragma unroll
-    for (int j = 0; j < KT / 16; ++j) {
-      if (chunk_base(kt * (KT / 16) + j) < 0) return false;
-    }
-    return true;
-  };
-  // Loop-invariant per-lane byte offsets inside a 16-key chunk; each load
-  // address is a wave-uniform chunk base (SGPRs) plus one of these, so no
-  // 64-bit per-lane address has to stay live (or spill) across the loop.
+  const int my_chunk = (w * IPW) / NC;   // every K and V block this wave loads lies in it
   const unsigned k_lane = 2u * (l16 * D + 8 * g4);             // K block, + 64cc bytes
   const int vq = lane & 31;                                     // V: read-lane pair
   const int v_key = 4 * (vq >> 3) + ((vq & 7) >> 1);           // key within the 16-key half
   const unsigned v_lane = 2u * (v_key * D + 16 * (lane >> 5) + 8 * (vq & 1));  // + 64mp bytes
-  auto issue_k = [&](int kt, char *buf) {
+  // Buffer resource over this wave's chunk of tile kt in `plane` (K or V
+  // pages): its size is the chunk's live rows, 0 past the context or for an
+  // unallocated page.  `win` is the window that starts at tile wkt.  Each
+  // load adds a lane offset (row * 2D + column bytes) and a scalar column
+  // offset; the column part stays below one 2D-byte row, so a lane's load is
+  // zero exactly when its row is not live.
+  auto chunk_rsrc = [&](const void *plane, int win, int wkt, int kt) {
+    const int key0 = (kt * MT + my_chunk) * 16;
+    const int rel = (key0 >> p.page_shift) - ((wkt * KT) >> p.page_shift);
+    const int phys = __builtin_amdgcn_readlane(win, rel);
+    const int live = phys < 0 ? 0 : min(16, context - key0);
+    const long base = phys < 0 ? 0 : ((((long)phys * p.KH + kh) << p.page_shift) | (key0 & (p.page - 1))) * (long)D;
+    // the resource must sit in SGPRs: make its wave-uniformity explicit
+    const char *addr = uniform_ptr((const char *)plane + 2 * base);
+    return __builtin_amdgcn_make_buffer_rsrc((void *)addr, (short)0, uniform(live > 0 ? live * D * 2 : 0),
+                                             kBufferWord3);
+  };
+  auto issue_k = [&](int win, int wkt, int kt, char *buf) {
+    const __amdgpu_buffer_rsrc_t r = chunk_rsrc(p.k, win, wkt, kt);
 #pragma unroll
     for (int j = 0; j < IPW; ++j) {
-      const int blk = w * IPW + j;                 // K block (mt, cc)
-      const int mt = blk / NC, cc = blk - mt * NC;
-      const long kb = chunk_base(kt * (KT / 16) + mt);
-      const char *src = uniform_ptr(kbytes + 2 * ((kb < 0 ? 0 : kb) + 32 * cc)) + k_lane;
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
-                                       (__attribute__((address_space(3))) void *)(buf + blk * 1024), 16,
-                                       0, 0);
+      const int blk = w * IPW + j;       // K block (mt, cc)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)(buf + blk * 1024), 16, k_lane, 64 * (blk % NC), 0, 0);
     }
   };
-  auto issue_v = [&](int kt, char *buf) {
+  auto issue_v = [&](int win, int wkt, int kt, char *buf) {
+    const __amdgpu_buffer_rsrc_t r = chunk_rsrc(p.v, win, wkt, kt);
 #pragma unroll
     for (int j = 0; j < IPW; ++j) {
-      const int blk = w * IPW + j;                 // V block pair (c2, h, mp), hc = 2*c2 + h
-      const int hc = blk / (MD / 2), mp = blk - hc * (MD / 2);
-      const long vb = chunk_base(kt * (KT / 16) + hc);
-      const char *src = uniform_ptr(vbytes + 2 * ((vb < 0 ? 0 : vb) + 32 * mp)) + v_lane;
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
-                                       (__attribute__((address_space(3))) void *)(buf + blk * 1024), 16,
-                                       0, 0);
+      const int blk = w * IPW + j;       // V block pair (hc, mp)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)(buf + blk * 1024), 16, v_lane,
+                                               64 * (blk % (MD / 2)), 0, 0);
     }
   };
-  // Dead keys of a partial tile: zero their V bytes so 0 * garbage cannot
-  // reach the P.V product (their logits are masked to -inf as well).
-  auto zero_dead = [&](int kt, char *vbuf) {
-    for (int i = tid; i < VBLK * 64; i += NT) {
-      const int blk = i >> 6, l = i & 63;
-      const int hc = blk / (MD / 2);
-      const int q = l & 31;
-      const int key = kt * KT + 16 * hc + 4 * (q >> 3) + ((q & 7) >> 1);
-      if (key >= context || chunk_base(key >> 4) < 0)
-        *(u32x4 *)(vbuf + blk * 1024 + 16 * l) = u32x4{0, 0, 0, 0};
+  // Wait for every load of this wave except the `recent` issued last, then
+  // barrier: all waves' older loads are visible and all waves have left the
+  // phase before.
+  auto sync = [&](int recent) {
+    if (recent >= 2 * IPW) {
+      __builtin_amdgcn_s_waitcnt((2 * IPW) | (0x7 << 4) | (0xF << 8));
+    } else if (recent >= IPW) {
+      __builtin_amdgcn_s_waitcnt(IPW | (0x7 << 4) | (0xF << 8));
+    } else {
+      __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xF << 8));
     }
-  };
-  auto tile_ready = [&]() {
-    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   };
 
-  // S^T = K Q^T for tile kt: lane holds keys 16mt + 4g4 + i for column l16.
-  // Dim chunk outer, key tile inner: consecutive MFMAs accumulate into
+  // ---- S^T = K Q^T: lane holds keys 16mt + 4g4 + i for column l16 ----
+  // Dim chunk outer, key chunk inner: consecutive MFMAs accumulate into
   // different registers, and the K operands of chunk cc+1 are read from LDS
   // while the MFMAs of chunk cc run.
-  auto compute_s = [&](const char *kt_lds, f32x4 (&sv)[KT / 16][NQ]) {
-    constexpr int MT = KT / 16;
+  f32x4 s[MT][NQ];
+  auto compute_s = [&](const char *kt_lds) {
     u32x4 a[MT], an[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       a[mt] = *(const u32x4 *)(kt_lds + (mt * NC + 0) * 1024 + 16 * lane);
 #pragma unroll
-      for (int nq = 0; nq < NQ; ++nq) sv[mt][nq] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int nq = 0; nq < NQ; ++nq) s[mt][nq] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc) {
@@ -316,7 +355,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREF
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-        for (int nq = 0; nq < NQ; ++nq) sv[mt][nq] = mfma<DT>(a[mt], qb[nq][cc], sv[mt][nq]);
+        for (int nq = 0; nq < NQ; ++nq) s[mt][nq] = mfma<DT>(a[mt], qb[nq][cc], s[mt][nq]);
       }
       if (cc + 1 < NC) {
 #pragma unroll
@@ -325,99 +364,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREF
     }
   };
 
-  f32x4 s_a[KT / 16][NQ], s_b[KT / 16][NQ];
-  // One pipelined step for tile kt.  kc / vc: LDS buffers of K(kt) / V(kt);
-  // kn / vn: the other pair (K(kt+1) already there, V(kt+1) to be loaded).
-  auto step = [&](int kt, char *kc, char *vc, char *kn, char *vn, f32x4 (&s)[KT / 16][NQ],
-                  f32x4 (&s_next)[KT / 16][NQ]) {
-    if constexpr (kPipeS) {
-      if (kt + 2 <= kt_last) issue_k(kt + 2, kc);
-      if (kt + 1 <= kt_last) {
-        issue_v(kt + 1, vn);
-        compute_s(kn, s_next);
-      }
-    } else {
-      if (kt + 1 <= kt_last) {
-        issue_k(kt + 1, kn);
-        issue_v(kt + 1, vn);
-      }
-      compute_s(kc, s);
-    }
-    const char *vt_lds = vc;
-
-    // ---- mask, online softmax per column ----
-    // A tile below every column's diagonal (and inside every window) needs
-    // no mask; the test is workgroup-uniform.  Columns past the segment keep
-    // finite logits and are never stored.  The running max is kept on raw
-    // logits (scale > 0) and the scale is folded into the exp argument.
-    const int kbase = kt * KT;
-    const bool full = kbase + KT - 1 <= start + r0 &&
-                      (p.window == 0 || kbase >= start + r0 + rows_here - p.window);
-    const float sc = p.scale_log2;
-    bool grew = false;
-    float alpha[NQ];
-#pragma unroll
-    for (int nq = 0; nq < NQ; ++nq) {
-      float mx = kNegInf;
-      if (full) {
-#pragma unroll
-        for (int mt = 0; mt < KT / 16; ++mt) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[mt][nq][i]);
-        }
-      } else {
-        const int lo = p.window > 0 ? qpos[nq] - p.window + 1 : -1;
-#pragma unroll
-        for (int mt = 0; mt < KT / 16; ++mt) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = kbase + 16 * mt + 4 * g4 + i;
-            const bool ok = (key <= qpos[nq]) & (key >= lo);
-            const float x = ok ? s[mt][nq][i] : kNegInf;
-            s[mt][nq][i] = x;
-            mx = fmaxf(mx, x);
-          }
-        }
-      }
-      mx = fmaxf(mx, shfl(mx, lane ^ 16));
-      mx = fmaxf(mx, shfl(mx, lane ^ 32));
-      const float mn = fmaxf(m_run[nq], mx);
-      grew |= mn > m_run[nq];
-      const float mu = mn == kNegInf ? 0.f : mn * sc;
-      alpha[nq] = __builtin_amdgcn_exp2f(m_run[nq] * sc - mu);
-      m_run[nq] = mn;
-      float ls = 0.f;
-#pragma unroll
-      for (int mt = 0; mt < KT / 16; ++mt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[mt][nq][i], sc, -mu));
-          s[mt][nq][i] = e;
-          ls += e;
-        }
-      }
-      l_run[nq] = l_run[nq] * alpha[nq] + ls;
-    }
-    // O is rescaled only when some column's running max grew in this tile
-    // (after the first tiles this is rare); the test is wave-uniform.
+  // ---- O^T += V^T P^T : keys contracted in the order of the S^T layout ----
+  // k-slot 8*g4 + j of a 32-key chunk c2 is key 32c2 + 4g4 + j (j < 4) or
+  // 32c2 + 16 + 4g4 + (j - 4): exactly the keys this lane's S^T registers
+  // of chunks 2c2 and 2c2+1 hold, and the keys the two transposing reads
+  // below return for rows 32c2 + 4g4 + (l16/4) and 16 further on.
+  u32x4 pb[C2][NQ];
+  auto compute_pv = [&](const char *vt_lds) {
+    // O is rescaled only when some column's running max moved in the
+    // softmax that produced P (rare after the first tile); wave-uniform.
     if (__builtin_amdgcn_ballot_w64(grew)) {
 #pragma unroll
       for (int nq = 0; nq < NQ; ++nq) {
 #pragma unroll
         for (int md = 0; md < MD; ++md) o[md][nq] *= alpha[nq];
       }
-    }
-
-    // ---- O^T += V^T P^T : keys contracted in the order of the S^T layout ----
-    // k-slot 8*g4 + j of a 32-key chunk c2 is key 32c2 + 4g4 + j (j < 4) or
-    // 32c2 + 16 + 4g4 + (j - 4): exactly the keys this lane's S^T registers
-    // of tiles 2c2 and 2c2+1 hold, and the keys the two transposing reads
-    // below return for rows 32c2 + 4g4 + (l16/4) and 16 further on.
-    u32x4 pb[KT / 32][NQ];
-#pragma unroll
-    for (int c2 = 0; c2 < KT / 32; ++c2) {
-#pragma unroll
-      for (int nq = 0; nq < NQ; ++nq) pb[c2][nq] = pack8<DT>(s[2 * c2][nq], s[2 * c2 + 1][nq]);
     }
     // V^T operand of (md, c2): half h of key chunk c2 lives in block pair
     // (2c2 + h, md/2); the operand of the next md is read while the MFMAs of
@@ -428,55 +389,149 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREF
       const u32x2 hi = read_tr16((const unsigned short *)(blk0 + (MD / 2) * 1024));
       return u32x4{lo[0], lo[1], hi[0], hi[1]};
     };
-    u32x4 va[KT / 32], vnx[KT / 32];
+    u32x4 va[C2], vnx[C2];
 #pragma unroll
-    for (int c2 = 0; c2 < KT / 32; ++c2) va[c2] = vop(0, c2);
+    for (int c2 = 0; c2 < C2; ++c2) va[c2] = vop(0, c2);
 #pragma unroll
     for (int md = 0; md < MD; ++md) {
       if (md + 1 < MD) {
 #pragma unroll
-        for (int c2 = 0; c2 < KT / 32; ++c2) vnx[c2] = vop(md + 1, c2);
+        for (int c2 = 0; c2 < C2; ++c2) vnx[c2] = vop(md + 1, c2);
       }
 #pragma unroll
-      for (int c2 = 0; c2 < KT / 32; ++c2) {
+      for (int c2 = 0; c2 < C2; ++c2) {
 #pragma unroll
         for (int nq = 0; nq < NQ; ++nq) o[md][nq] = mfma<DT>(va[c2], pb[c2][nq], o[md][nq]);
       }
       if (md + 1 < MD) {
 #pragma unroll
-        for (int c2 = 0; c2 < KT / 32; ++c2) va[c2] = vnx[c2];
-      }
-    }
-    if (kt < kt_last) {
-      tile_ready();  // K(kt+2) and V(kt+1) landed; every wave is done with kt
-      if (!whole(kt + 1)) {
-        zero_dead(kt + 1, vn);
-        __syncthreads();
+        for (int c2 = 0; c2 < C2; ++c2) va[c2] = vnx[c2];
       }
     }
   };
 
-  issue_k(kt_first, s_k0);
-  if (kPipeS && kt_first < kt_last) issue_k(kt_first + 1, s_k1);
-  issue_v(kt_first, s_v0);
-  tile_ready();
-  if (!whole(kt_first)) {
-    zero_dead(kt_first, s_v0);
-    __syncthreads();
+  // ---- mask + online softmax of S(kt) into P(kt) ----
+  // A tile below every column's diagonal (and inside every window) needs no
+  // mask; the test is workgroup-uniform.  Columns past the segment keep
+  // finite logits and are never stored.  The running max is kept on raw
+  // logits (scale > 0) and only moved when a tile's max exceeds it by more
+  // than kMaxSlack in the exp2 domain.
+  const float sc = p.scale_log2;
+  const float slack = kMaxSlack / sc;
+  auto softmax = [&](int kt) {
+    const int kbase = kt * KT;
+    const bool full = kbase + KT - 1 <= start + r0 &&
+                      (p.window == 0 || kbase >= start + r0 + rows_here - p.window);
+    grew = false;
+#pragma unroll
+    for (int nq = 0; nq < NQ; ++nq) {
+      float mx = kNegInf;
+      if (full) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[mt][nq][i]);
+        }
+      } else {
+        const int lo = p.window > 0 ? qpos[nq] - p.window + 1 : -1;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = kbase + 16 * mt + 4 * g4 + i;
+            const bool ok = (key <= qpos[nq]) & (key >= lo);
+            const float x = ok ? s[mt][nq][i] : kNegInf;
+            s[mt][nq][i] = x;
+            mx = fmaxf(mx, x);
+          }
+        }
+      }
+      // max over the four lanes of this column (l16, +16, +32, +48)
+      mx = xor32_max(xor16_max(mx));
+      const bool up = mx > m_run[nq] + slack;  // m_run = -inf moves to any finite max
+      grew |= up;
+      const float mn = up ? mx : m_run[nq];
+      const float mu = mn == kNegInf ? 0.f : mn * sc;
+      alpha[nq] = up ? __builtin_amdgcn_exp2f(m_run[nq] * sc - mu) : 1.f;
+      m_run[nq] = mn;
+      float ls = 0.f;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[mt][nq][i], sc, -mu));
+          s[mt][nq][i] = e;
+          ls += e;
+        }
+      }
+      l_run[nq] = l_run[nq] * alpha[nq] + ls;
+    }
+#pragma unroll
+    for (int c2 = 0; c2 < C2; ++c2) {
+#pragma unroll
+      for (int nq = 0; nq < NQ; ++nq) pb[c2][nq] = pack8<DT>(s[2 * c2][nq], s[2 * c2 + 1][nq]);
+    }
+  };
+
+  // `win` holds the page-table window of tiles kt+1 and kt+2 on entry to
+  // step kt and of tiles kt+2 and kt+3 on exit.
+  int win;
+  // One tile: kc = K(kt), vp = V(kt-1), kw / vw receive K(kt+2) / V(kt+1).
+  auto step = [&](int kt, const char *kc, const char *vp, char *kw, char *vw) {
+    int issued = 0;
+    if (kt + 2 <= kt_last) {
+      issue_k(win, kt + 1, kt + 2, kw);
+      issued += IPW;
+    }
+    if (kt + 1 <= kt_last) {
+      issue_v(win, kt + 1, kt + 1, vw);
+      issued += IPW;
+    }
+    win = read_window(kt + 2);
+    compute_s(kc);
+    if (kt > kt_first) compute_pv(vp);
+#ifndef DD_PREFILL_MIDSYNC
+#define DD_PREFILL_MIDSYNC 0
+#endif
+    if (DD_PREFILL_MIDSYNC) sync(issued);
+    softmax(kt);
+    sync(issued);
+  };
+
+  // Prologue: K(first) alone, then K(first+1) and V(first) as if issued by
+  // the M phase of tile first-1.
+  win = read_window(kt_first);
+  issue_k(win, kt_first, kt_first, s_k0);
+  int issued = 0;
+  if (kt_first + 1 <= kt_last) {
+    issue_k(win, kt_first, kt_first + 1, s_k1);
+    issued += IPW;
   }
-  if constexpr (kPipeS) compute_s(s_k0, s_a);
-  for (int kt = kt_first; kt <= kt_last; kt += 2) {
-    step(kt, s_k0, s_v0, s_k1, s_v1, s_a, s_b);
-    if (kt + 1 <= kt_last) step(kt + 1, s_k1, s_v1, s_k0, s_v0, s_b, s_a);
+  issue_v(win, kt_first, kt_first, s_v0);
+  issued += IPW;
+  sync(issued);
+  win = read_window(kt_first + 1);
+  if (kPingPong && w >= 4) __syncthreads();  // second group: one phase behind
+
+  for (int kt = kt_first; kt <= kt_last; kt += 3) {
+    step(kt, s_k0, s_v2, s_k2, s_v1);
+    if (kt + 1 <= kt_last) step(kt + 1, s_k1, s_v0, s_k0, s_v2);
+    if (kt + 2 <= kt_last) step(kt + 2, s_k2, s_v1, s_k1, s_v0);
   }
+  // P.V of the last tile; its V was waited for before the last barrier.
+  switch ((kt_last - kt_first) % 3) {
+    case 0: compute_pv(s_v0); break;
+    case 1: compute_pv(s_v1); break;
+    default: compute_pv(s_v2); break;
+  }
+  if (kPingPong && w < 4) __syncthreads();  // same barrier count for both groups
 
   // ---- normalise and store: lane holds dims 16md + 4g4 + i of its column ----
   unsigned short *dst = (unsigned short *)p.out;
 #pragma unroll
   for (int nq = 0; nq < NQ; ++nq) {
     float l = l_run[nq];
-    l += shfl(l, lane ^ 16);
-    l += shfl(l, lane ^ 32);
+    l = xor32_sum(xor16_sum(l));
     if (!colok[nq]) continue;
     const float inv = 1.f / l;
     const int c = w * 16 * NQ + nq * 16 + l16;
@@ -493,10 +548,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREF
 }
 
 template <int DT, int D, int NQ, int KT, int NW>
-int launch(PrefillParams p, int max_len, hipStream_t s) {
+int launch(PrefillParams p, int max_len, int plan_len, hipStream_t s) {
   if (16 * NQ * NW / p.G < 1) return DD_EUNSUPPORTED;
   p.max_tiles = (int)dd_cdiv(max_len, (16 * NQ * NW) / p.G);
-  const long grid = 8L * dd_cdiv((long)p.n * p.KH, 8) * p.max_tiles;
+  const long grid = p.plan ? (long)plan_len : 8L * dd_cdiv((long)p.n * p.KH, 8) * p.max_tiles;
   if (grid == 0) return DD_OK;
   if (grid > 0x7fffffffL) return DD_EUNSUPPORTED;
   hipLaunchKernelGGL((prefill_kernel<DT, D, NQ, KT, NW>), dim3((unsigned)grid), dim3(64 * NW), 0, s, p);
@@ -504,12 +559,31 @@ int launch(PrefillParams p, int max_len, hipStream_t s) {
   return DD_OK;
 }
 
-template <int DT>
-int dispatch(const PrefillParams &p, int D, int max_len, hipStream_t s) {
+// Tile geometry per head dim: (query row, head) columns per workgroup and
+// keys per tile.  The kernel instantiations below and the host-side plan
+// both read it from here.
+struct Geometry {
+  int cols, kt;
+};
+constexpr Geometry kGeom64{16 * 2 * DD_PREFILL_NW, 64};
+constexpr Geometry kGeom128{16 * DD_PREFILL_NQ128 * DD_PREFILL_NW, 64};
+constexpr Geometry kGeom256{16 * 1 * DD_PREFILL_NW, 32};
+
+static bool geometry(int D, Geometry *g) {
   switch (D) {
-    case 64: return launch<DT, 64, 2, 64, DD_PREFILL_NW>(p, max_len, s);
-    case 128: return launch<DT, 128, DD_PREFILL_NQ128, 64, DD_PREFILL_NW>(p, max_len, s);
-    case 256: return launch<DT, 256, 1, 32, 4>(p, max_len, s);
+    case 64: *g = kGeom64; return true;
+    case 128: *g = kGeom128; return true;
+    case 256: *g = kGeom256; return true;
+    default: return false;
+  }
+}
+
+template <int DT>
+int dispatch(const PrefillParams &p, int D, int max_len, int plan_len, hipStream_t s) {
+  switch (D) {
+    case 64: return launch<DT, 64, 2, kGeom64.kt, DD_PREFILL_NW>(p, max_len, plan_len, s);
+    case 128: return launch<DT, 128, DD_PREFILL_NQ128, kGeom128.kt, DD_PREFILL_NW>(p, max_len, plan_len, s);
+    case 256: return launch<DT, 256, 1, kGeom256.kt, DD_PREFILL_NW>(p, max_len, plan_len, s);
     default: return DD_EUNSUPPORTED;
   }
 }
@@ -521,12 +595,13 @@ extern "C" int dd_prefill_attention(const void *q, const void *k, const void *v,
                                     int max_context,
                                     const int32_t *page_table, int table_rows, int table_width, int heads,
                                     int kv_heads, int dim, int page_size, int64_t capacity, int window, float scale,
-                                    void *out, void *stream) {
+                                    const int32_t *plan, int plan_len, void *out, void *stream) {
   if (!q || !k || !v || !cu_seqlens || !context_lens || !slots || !page_table || !out || n < 0 || max_len < 0 ||
       heads <= 0 || kv_heads <= 0 || heads % kv_heads || page_size <= 0 || capacity <= 0 || table_width <= 0)
     return DD_EINVAL;
   if (heads / kv_heads > 16) return DD_EUNSUPPORTED;
   if ((long)max_context > (long)kTabCache * page_size) return DD_EUNSUPPORTED;
+  if (plan && plan_len <= 0) return DD_EINVAL;
   if (n == 0 || max_len == 0) return DD_OK;
   PrefillParams p{};
   p.q = q;
@@ -536,6 +611,7 @@ extern "C" int dd_prefill_attention(const void *q, const void *k, const void *v,
   p.ctx = context_lens;
   p.slots = slots;
   p.table = page_table;
+  p.plan = plan;
   p.out = out;
   p.capacity = capacity;
   p.n = n;
@@ -551,7 +627,73 @@ extern "C" int dd_prefill_attention(const void *q, const void *k, const void *v,
   p.window = window > 0 ? window : 0;
   p.scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == DD_BF16) return dispatch<DD_BF16>(p, dim, max_len, s);
-  if (dtype == DD_F16) return dispatch<DD_F16>(p, dim, max_len, s);
+  if (dtype == DD_BF16) return dispatch<DD_BF16>(p, dim, max_len, plan_len, s);
+  if (dtype == DD_F16) return dispatch<DD_F16>(p, dim, max_len, plan_len, s);
   return DD_EUNSUPPORTED;
+}
+
+// Workgroup order for dd_prefill_attention, computed on the host from the
+// host copy of the segment lengths and starts.  A work item is one
+// (segment, KV head, query tile); its cost is the number of key tiles it
+// visits plus a fixed start-up charge.  Groups (segment, KV head) are spread
+// over the 8 XCDs longest-processing-time first, so that every query tile of
+// a group shares one XCD's L2; within an XCD the items run longest first.
+// Workgroup b is dispatched to XCD b % 8, so plan[8 j + x] is the j-th item
+// of XCD x (-1 pads the shorter XCD lists).
+extern "C" int dd_prefill_plan(const int64_t *lengths, const int64_t *starts, int n, int heads, int kv_heads,
+                               int dim, int window, int32_t *plan, int capacity) {
+  if (!lengths || !starts || n < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || capacity < 0)
+    return -DD_EINVAL;
+  Geometry g;
+  if (!geometry(dim, &g)) return -DD_EUNSUPPORTED;
+  const int G = heads / kv_heads;
+  const int rows = g.cols / G;
+  if (rows < 1) return -DD_EUNSUPPORTED;
+  long max_len = 0;
+  for (int i = 0; i < n; ++i) {
+    if (lengths[i] < 0 || starts[i] < 0) return -DD_EINVAL;
+    max_len = std::max<long>(max_len, lengths[i]);
+  }
+  const long max_tiles = dd_cdiv(max_len, rows);
+  if ((long)n * kv_heads * std::max<long>(max_tiles, 1) > 0x7fffffffL) return -DD_EUNSUPPORTED;
+  constexpr long kStartup = 2;  // charge of a workgroup's prologue and epilogue, in key tiles
+  auto item_cost = [&](int seg, long qt) {
+    const long r0 = qt * rows;
+    const long here = std::min<long>(rows, lengths[seg] - r0);
+    const long k_hi = starts[seg] + r0 + here;
+    const long k_lo = window > 0 ? std::max<long>(0, starts[seg] + r0 - window + 1) : 0;
+    return (k_hi - 1) / g.kt - k_lo / g.kt + 1 + kStartup;
+  };
+  // groups, heaviest first, each to the least-loaded XCD
+  std::vector<std::pair<long, int>> groups;  // (-cost, group)
+  for (int seg = 0; seg < n; ++seg) {
+    const long tiles = dd_cdiv(lengths[seg], rows);
+    long cost = 0;
+    for (long qt = 0; qt < tiles; ++qt) cost += item_cost(seg, qt);
+    if (tiles == 0) continue;
+    for (int kh = 0; kh < kv_heads; ++kh) groups.push_back({-cost, seg * kv_heads + kh});
+  }
+  std::sort(groups.begin(), groups.end());
+  constexpr int kXcds = 8;
+  long load[kXcds] = {};
+  std::vector<std::vector<std::pair<long, int>>> lists(kXcds);  // (-cost, item)
+  for (const auto &gr : groups) {
+    const int x = (int)(std::min_element(load, load + kXcds) - load);
+    load[x] -= gr.first;
+    const int seg = gr.second / kv_heads;
+    const long tiles = dd_cdiv(lengths[seg], rows);
+    for (long qt = 0; qt < tiles; ++qt)
+      lists[x].push_back({-item_cost(seg, qt), (int)(gr.second * max_tiles + qt)});
+  }
+  size_t longest = 0;
+  for (auto &l : lists) {
+    std::stable_sort(l.begin(), l.end());
+    longest = std::max(longest, l.size());
+  }
+  const long need = (long)kXcds * (long)longest;
+  if (need > 0x7fffffffL) return -DD_EUNSUPPORTED;
+  if (!plan || capacity < need) return (int)need;
+  for (size_t j = 0; j < longest; ++j)
+    for (int x = 0; x < kXcds; ++x) plan[kXcds * j + x] = j < lists[x].size() ? lists[x][j].second : -1;
+  return (int)need;
 }

@@ -9,6 +9,9 @@ place: multi-token segments by the paged MFMA prefill kernel, the trailing
 run of single-token segments by the split-KV decode kernel.  Both read the
 pages directly; nothing is gathered.
 """
+import ctypes
+
+import numpy as np
 import torch
 
 from . import _native, kernels
@@ -31,6 +34,29 @@ def _check(query, cache_k, cache_v, page_table):
     return query
 
 
+def prefill_plan(lengths, starts, heads, kv_heads, dim, window=0):
+    """Workgroup order of the prefill kernel for these segments (host int32).
+
+    Balances (segment, KV head, query tile) items over the XCDs, longest
+    first, from the host copies of the segment lengths and starts.
+    """
+    lengths = np.ascontiguousarray(lengths, dtype=np.int64)
+    starts = np.ascontiguousarray(starts, dtype=np.int64)
+    if lengths.shape != starts.shape or lengths.ndim != 1:
+        raise ValueError('lengths and starts must be matching 1-D sequences')
+    lib = _native.library()
+    args = (lengths.ctypes.data_as(ctypes.c_void_p), starts.ctypes.data_as(ctypes.c_void_p), len(lengths),
+            heads, kv_heads, dim, int(window or 0))
+    need = lib.dd_prefill_plan(*args, None, 0)
+    if need < 0:
+        raise _native.NativeError(f'dd_prefill_plan failed: {lib.dd_error_string(-need).decode()} ({-need})')
+    plan = np.empty(max(need, 1), dtype=np.int32)
+    got = lib.dd_prefill_plan(*args, plan.ctypes.data_as(ctypes.c_void_p), len(plan))
+    if got != need:
+        raise _native.NativeError('dd_prefill_plan returned an inconsistent length')
+    return plan[:need]
+
+
 def prefill_attention(query, cache_k, cache_v, packed, page_table, window=0, scale=None, out=None,
                       segments=None):
     """Causal attention of every packed query token over its slot's pages.
@@ -49,11 +75,15 @@ def prefill_attention(query, cache_k, cache_v, packed, page_table, window=0, sca
     max_context = max(s + n for s, n in zip(packed.starts[a:b], packed.lengths[a:b]))
     if max_context > 8192 * cache_k.shape[2]:
         raise ValueError('prefill attention supports up to 8192 pages of history per segment')
+    plan = prefill_plan(packed.lengths[a:b], packed.starts[a:b], H, cache_k.shape[1], D, window)
+    if len(plan) == 0:
+        return out
+    plan_dev = torch.from_numpy(plan).pin_memory().to(q.device, non_blocking=True)
     call('dd_prefill_attention', ptr(q), ptr(cache_k), ptr(cache_v), DTYPE_CODES[q.dtype],
          ptr(packed.cu_seqlens[a:]), ptr(packed.context_lens[a:]), ptr(packed._meta[2, a:]), b - a, max_len, max_context,
          ptr(page_table), page_table.shape[0], page_table.shape[1], H, cache_k.shape[1], D, cache_k.shape[2],
-         cache_k.shape[0], int(window or 0), float(D ** -.5 if scale is None else scale), ptr(out),
-         _native.stream_of(q))
+         cache_k.shape[0], int(window or 0), float(D ** -.5 if scale is None else scale),
+         ptr(plan_dev), len(plan), ptr(out), _native.stream_of(q))
     return out
 
 

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define DD_ABI_VERSION 1
+#define DD_ABI_VERSION 2
 
 enum dd_dtype { DD_F32 = 0, DD_F16 = 1, DD_BF16 = 2, DD_I8 = 3 };
 
@@ -224,6 +224,9 @@ int dd_rope_batch(const void *qkv, int qkv_dtype, const void *cos,
  *   cu_seqlens    int64 (n+1), context_lens int64 (n) = start+len, slots int64 (n)
  *   max_len       the longest segment (sizes the grid)
  *   max_context   the longest start+len; at most 8192 pages per segment
+ *   plan          NULL, or the device copy of dd_prefill_plan's output for
+ *                 these same lengths/starts (plan_len entries): the
+ *                 workgroup order; NULL uses a fixed XCD-aware order
  * Row j of segment i attends keys 0 .. start_i + j (and > that - window).
  */
 int dd_prefill_attention(const void *q, const void *k, const void *v,
@@ -233,8 +236,20 @@ int dd_prefill_attention(const void *q, const void *k, const void *v,
                          const int32_t *page_table,
                          int table_rows, int table_width, int heads,
                          int kv_heads, int dim, int page_size,
-                         int64_t capacity, int window, float scale, void *out,
+                         int64_t capacity, int window, float scale,
+                         const int32_t *plan, int plan_len, void *out,
                          void *stream);
+
+/*
+ * Host-side schedule for dd_prefill_attention (no reference counterpart:
+ * the reference runs one SDPA per segment, paged.py:97-111).  lengths and
+ * starts are HOST int64 arrays (n).  Writes the workgroup order to plan
+ * (host int32, capacity entries) and returns its length; with plan == NULL
+ * or too small a capacity it only returns the length.  Negative = -DD_E*.
+ */
+int dd_prefill_plan(const int64_t *lengths, const int64_t *starts, int n,
+                    int heads, int kv_heads, int dim, int window,
+                    int32_t *plan, int capacity);
 
 /*
  * Index plans of damendaemon/cache_indices.py:24-80 (DeepSeek-style

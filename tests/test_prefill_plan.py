@@ -1,0 +1,72 @@
+"""Host-side prefill schedule (dd_prefill_plan): runs on the CPU."""
+import random
+
+import numpy as np
+import pytest
+
+from damendaemon_amd import ragged
+
+ROWS = {64: 256, 128: 256, 256: 64}   # (query row, head) columns per workgroup
+KT = {64: 64, 128: 64, 256: 32}       # keys per tile
+
+
+def _items(lengths, starts, heads, kv_heads, dim, window):
+    rows = ROWS[dim] // (heads // kv_heads)
+    max_tiles = -(-max(lengths) // rows) if lengths else 0
+    cost = {}
+    for seg, (n, s) in enumerate(zip(lengths, starts)):
+        for kh in range(kv_heads):
+            for qt in range(-(-n // rows)):
+                r0 = qt * rows
+                k_hi = s + r0 + min(rows, n - r0)
+                k_lo = max(0, s + r0 - window + 1) if window > 0 else 0
+                cost[(seg * kv_heads + kh) * max_tiles + qt] = (k_hi - 1) // KT[dim] - k_lo // KT[dim] + 1
+    return cost, max_tiles
+
+
+@pytest.mark.parametrize('seed', range(6))
+def test_plan_covers_every_tile_once_grouped_per_xcd_longest_first(seed):
+    rng = random.Random(seed)
+    dim = rng.choice([64, 128, 256])
+    kv_heads = rng.choice([1, 2, 8])
+    heads = kv_heads * rng.choice([1, 4, 8])
+    n = rng.randint(1, 12)
+    lengths = [rng.choice([1, 7, 64, 300, 512, 1000]) for _ in range(n)]
+    starts = [rng.randint(0, 5000) for _ in range(n)]
+    window = rng.choice([0, 0, 700])
+    plan = ragged.prefill_plan(lengths, starts, heads, kv_heads, dim, window)
+    cost, max_tiles = _items(lengths, starts, heads, kv_heads, dim, window)
+    assert plan.dtype == np.int32 and len(plan) % 8 == 0
+    real = plan[plan >= 0].tolist()
+    assert sorted(real) == sorted(cost)             # every item exactly once
+    xcd_of_group = {}
+    for x in range(8):
+        lst = [int(i) for i in plan[x::8]]
+        seen_pad = False
+        prev = None
+        for item in lst:
+            if item < 0:
+                seen_pad = True
+                continue
+            assert not seen_pad                      # padding only at the end
+            grp = item // max_tiles
+            assert xcd_of_group.setdefault(grp, x) == x
+            assert prev is None or cost[item] <= prev
+            prev = cost[item]
+
+
+def test_plan_balances_xcds():
+    lengths = [512] * 8
+    starts = [3198, 2211, 2253, 3990, 2141, 2468, 3884, 968]
+    plan = ragged.prefill_plan(lengths, starts, 32, 8, 128, 0)
+    cost, _ = _items(lengths, starts, 32, 8, 128, 0)
+    loads = [sum(cost[i] for i in plan[x::8] if i >= 0) for x in range(8)]
+    assert max(loads) <= 1.2 * min(loads)
+
+
+def test_plan_rejects_bad_arguments():
+    with pytest.raises(Exception):
+        ragged.prefill_plan([4], [0], 6, 4, 128)     # heads not a multiple of kv_heads
+    with pytest.raises(Exception):
+        ragged.prefill_plan([4], [0], 8, 2, 96)      # no prefill kernel for head dim 96
+    assert len(ragged.prefill_plan([], [], 8, 2, 128)) == 0
