@@ -632,6 +632,15 @@ extern "C" int dd_prefill_attention(const void *q, const void *k, const void *v,
   return DD_EUNSUPPORTED;
 }
 
+extern "C" int dd_prefill_geometry(int dim, int *columns, int *keys_per_tile) {
+  Geometry g;
+  if (!columns || !keys_per_tile) return DD_EINVAL;
+  if (!geometry(dim, &g)) return DD_EUNSUPPORTED;
+  *columns = g.cols;
+  *keys_per_tile = g.kt;
+  return DD_OK;
+}
+
 // Workgroup order for dd_prefill_attention, computed on the host from the
 // host copy of the segment lengths and starts.  A work item is one
 // (segment, KV head, query tile); its cost is the number of key tiles it

@@ -252,6 +252,12 @@ int dd_prefill_plan(const int64_t *lengths, const int64_t *starts, int n,
                     int32_t *plan, int capacity);
 
 /*
+ * Tile geometry of dd_prefill_attention for head size dim: (query row,
+ * head) columns per workgroup and keys per tile (host-side query).
+ */
+int dd_prefill_geometry(int dim, int *columns, int *keys_per_tile);
+
+/*
  * Index plans of damendaemon/cache_indices.py:24-80 (DeepSeek-style
  * windowed + compressed-block attention), int64, -1 = padding.
  * dd_prefill_indices: out (query_stop - query_start, min(window, seq_len)

@@ -1,13 +1,22 @@
 """Host-side prefill schedule (dd_prefill_plan): runs on the CPU."""
+import ctypes
 import random
 
 import numpy as np
 import pytest
 
-from damendaemon_amd import ragged
+from damendaemon_amd import _native, ragged
 
-ROWS = {64: 256, 128: 256, 256: 64}   # (query row, head) columns per workgroup
-KT = {64: 64, 128: 64, 256: 32}       # keys per tile
+
+
+def _geometry(dim):
+    cols, kt = ctypes.c_int(), ctypes.c_int()
+    assert _native.library().dd_prefill_geometry(dim, ctypes.byref(cols), ctypes.byref(kt)) == 0
+    return cols.value, kt.value
+
+
+ROWS = {d: _geometry(d)[0] for d in (64, 128, 256)}   # (query row, head) columns per workgroup
+KT = {d: _geometry(d)[1] for d in (64, 128, 256)}     # keys per tile
 
 
 def _items(lengths, starts, heads, kv_heads, dim, window):
@@ -70,3 +79,5 @@ def test_plan_rejects_bad_arguments():
     with pytest.raises(Exception):
         ragged.prefill_plan([4], [0], 8, 2, 96)      # no prefill kernel for head dim 96
     assert len(ragged.prefill_plan([], [], 8, 2, 128)) == 0
+    cols, kt = ctypes.c_int(), ctypes.c_int()
+    assert _native.library().dd_prefill_geometry(96, ctypes.byref(cols), ctypes.byref(kt)) != 0
