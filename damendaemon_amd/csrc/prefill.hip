@@ -27,6 +27,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <vector>
 
 // The running max of a column is only moved when a tile's max exceeds it by
@@ -129,26 +130,16 @@ DD_DEV unsigned pack2(float a, float b) {
 // The direct-to-LDS loads fill these blocks: DMA lane l of a V block pair
 // covers read lanes 2(l%32), 2(l%32)+1 of half l/32 (16 contiguous bytes).
 //
-// Schedule.  Tile t is processed in two phases separated by workgroup
-// barriers: M(t) issues the loads of K(t+2) and V(t+1), computes S(t) =
-// K(t) Q^T and O += V(t-1)^T P(t-1)^T (all MFMA), and V(t) runs the online
-// softmax of S(t) into P(t) (all VALU).  With 8 waves the second four
-// (one per SIMD) run one barrier behind the first four, so on every SIMD
-// one wave is in an MFMA phase while the other is in a VALU phase.
-// Hazards, with both groups one phase apart: K(t) is read in M(t) and
-// V(t-1) in M(t) only, so K(t+2) may overwrite K(t-1) and V(t+1) may
-// overwrite V(t-2) once every wave has left M(t-1): three K and three V
-// buffers.  A wave issues its loads at the start of M(t) and, before each
-// barrier, waits for all of its loads except the ones issued in the current
-// M phase, which gives K(t) and V(t-1) two to four phases to land before
-// the first wave reads them.
+// Schedule.  K and V tiles rotate through three LDS buffers each.  Step t
+// issues the loads of tile t+2 into the buffers of tile t-1 (every wave left
+// them at the previous barrier), computes S(t) = K(t) Q^T, the online
+// softmax and O += V(t)^T P(t)^T, then waits for its own loads of tile t+1
+// and meets the other waves at a barrier: a tile's loads have about two
+// steps to land.  The two waves that share a SIMD overlap one's MFMAs with
+// the other's softmax.
 // Keys past the context and chunks without an allocated page are loaded as
 // zeros: every chunk load goes through a buffer resource whose size covers
 // only the chunk's live rows (out-of-range buffer loads return 0).
-
-#ifndef DD_PREFILL_WAVES
-#define DD_PREFILL_WAVES 2
-#endif
 
 // 32-bit word 3 of a raw (untyped) buffer resource.
 constexpr int kBufferWord3 = 0x00020000;
@@ -156,7 +147,7 @@ constexpr int kBufferWord3 = 0x00020000;
 typedef __attribute__((address_space(3))) void lds_void;
 
 template <int DT, int D, int NQ, int KT, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREFILL_WAVES))) void prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4))) void prefill_kernel(PrefillParams p) {
   constexpr int NC = D / 32;           // k-chunks of q.k
   constexpr int MD = D / 16;           // O^T row tiles
   constexpr int MT = KT / 16;          // 16-key chunks per tile
@@ -170,10 +161,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREF
   constexpr int IPW = KBLK / NW;       // DMA instructions per wave per plane
   static_assert(NC % IPW == 0 && MD / 2 == NC, "a wave's blocks share one 16-key chunk");
   static_assert(2 * IPW < 16, "vmcnt immediate");
-#ifndef DD_PREFILL_PINGPONG
-#define DD_PREFILL_PINGPONG 0
-#endif
-  constexpr bool kPingPong = DD_PREFILL_PINGPONG && NW == 8;  // waves w and w+4 share a SIMD
 
   // Six distinct buffers (three K, three V).  Every direct-to-LDS load and
   // every LDS read below names one of them at compile time (the tile loop is
@@ -291,7 +278,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREF
   // load adds a lane offset (row * 2D + column bytes) and a scalar column
   // offset; the column part stays below one 2D-byte row, so a lane's load is
   // zero exactly when its row is not live.
-  auto chunk_rsrc = [&](const void *plane, int win, int wkt, int kt) {
+  auto chunk_rsrc = [&](const void *plane, int win, int wkt, int kt) __attribute__((always_inline)) __attribute__((always_inline)) {
     const int key0 = (kt * MT + my_chunk) * 16;
     const int rel = (key0 >> p.page_shift) - ((wkt * KT) >> p.page_shift);
     const int phys = __builtin_amdgcn_readlane(win, rel);
@@ -302,7 +289,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREF
     return __builtin_amdgcn_make_buffer_rsrc((void *)addr, (short)0, uniform(live > 0 ? live * D * 2 : 0),
                                              kBufferWord3);
   };
-  auto issue_k = [&](int win, int wkt, int kt, char *buf) {
+  auto issue_k = [&](int win, int wkt, int kt, char *buf) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t r = chunk_rsrc(p.k, win, wkt, kt);
 #pragma unroll
     for (int j = 0; j < IPW; ++j) {
@@ -310,7 +297,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREF
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)(buf + blk * 1024), 16, k_lane, 64 * (blk % NC), 0, 0);
     }
   };
-  auto issue_v = [&](int win, int wkt, int kt, char *buf) {
+  auto issue_v = [&](int win, int wkt, int kt, char *buf) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t r = chunk_rsrc(p.v, win, wkt, kt);
 #pragma unroll
     for (int j = 0; j < IPW; ++j) {
@@ -322,7 +309,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREF
   // Wait for every load of this wave except the `recent` issued last, then
   // barrier: all waves' older loads are visible and all waves have left the
   // phase before.
-  auto sync = [&](int recent) {
+  auto sync = [&](int recent) __attribute__((always_inline)) {
     if (recent >= 2 * IPW) {
       __builtin_amdgcn_s_waitcnt((2 * IPW) | (0x7 << 4) | (0xF << 8));
     } else if (recent >= IPW) {
@@ -338,28 +325,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREF
   // different registers, and the K operands of chunk cc+1 are read from LDS
   // while the MFMAs of chunk cc run.
   f32x4 s[MT][NQ];
-  auto compute_s = [&](const char *kt_lds) {
-    u32x4 a[MT], an[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      a[mt] = *(const u32x4 *)(kt_lds + (mt * NC + 0) * 1024 + 16 * lane);
-#pragma unroll
-      for (int nq = 0; nq < NQ; ++nq) s[mt][nq] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+  auto compute_s = [&](const char *kt_lds) __attribute__((always_inline)) {
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc) {
-      if (cc + 1 < NC) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) an[mt] = *(const u32x4 *)(kt_lds + (mt * NC + cc + 1) * 1024 + 16 * lane);
-      }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
+        const u32x4 a = *(const u32x4 *)(kt_lds + (mt * NC + cc) * 1024 + 16 * lane);
 #pragma unroll
-        for (int nq = 0; nq < NQ; ++nq) s[mt][nq] = mfma<DT>(a[mt], qb[nq][cc], s[mt][nq]);
-      }
-      if (cc + 1 < NC) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) a[mt] = an[mt];
+        for (int nq = 0; nq < NQ; ++nq)
+          s[mt][nq] = mfma<DT>(a, qb[nq][cc], cc == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : s[mt][nq]);
       }
     }
   };
@@ -370,7 +344,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREF
   // of chunks 2c2 and 2c2+1 hold, and the keys the two transposing reads
   // below return for rows 32c2 + 4g4 + (l16/4) and 16 further on.
   u32x4 pb[C2][NQ];
-  auto compute_pv = [&](const char *vt_lds) {
+  auto compute_pv = [&](const char *vt_lds) __attribute__((always_inline)) {
     // O is rescaled only when some column's running max moved in the
     // softmax that produced P (rare after the first tile); wave-uniform.
     if (__builtin_amdgcn_ballot_w64(grew)) {
@@ -418,33 +392,38 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREF
   // than kMaxSlack in the exp2 domain.
   const float sc = p.scale_log2;
   const float slack = kMaxSlack / sc;
-  auto softmax = [&](int kt) {
+  auto tile_full = [&](int kt) __attribute__((always_inline)) {
     const int kbase = kt * KT;
-    const bool full = kbase + KT - 1 <= start + r0 &&
-                      (p.window == 0 || kbase >= start + r0 + rows_here - p.window);
+    return kbase + KT - 1 <= start + r0 && (p.window == 0 || kbase >= start + r0 + rows_here - p.window);
+  };
+  // Logits of keys past a column's diagonal or before its window become
+  // -inf; applied (rarely) to a tile's S right after it is computed, so the
+  // softmax itself is straight-line code.
+  auto mask_s = [&](int kt) __attribute__((always_inline)) {
+    const int kbase = kt * KT;
+#pragma unroll
+    for (int nq = 0; nq < NQ; ++nq) {
+      const int lo = p.window > 0 ? qpos[nq] - p.window + 1 : -1;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kbase + 16 * mt + 4 * g4 + i;
+          const bool ok = (key <= qpos[nq]) & (key >= lo);
+          s[mt][nq][i] = ok ? s[mt][nq][i] : kNegInf;
+        }
+      }
+    }
+  };
+  auto softmax = [&]() __attribute__((always_inline)) {
     grew = false;
 #pragma unroll
     for (int nq = 0; nq < NQ; ++nq) {
       float mx = kNegInf;
-      if (full) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
+      for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[mt][nq][i]);
-        }
-      } else {
-        const int lo = p.window > 0 ? qpos[nq] - p.window + 1 : -1;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = kbase + 16 * mt + 4 * g4 + i;
-            const bool ok = (key <= qpos[nq]) & (key >= lo);
-            const float x = ok ? s[mt][nq][i] : kNegInf;
-            s[mt][nq][i] = x;
-            mx = fmaxf(mx, x);
-          }
-        }
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[mt][nq][i]);
       }
       // max over the four lanes of this column (l16, +16, +32, +48)
       mx = xor32_max(xor16_max(mx));
@@ -469,62 +448,50 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DD_PREF
 #pragma unroll
     for (int c2 = 0; c2 < C2; ++c2) {
 #pragma unroll
-      for (int nq = 0; nq < NQ; ++nq) pb[c2][nq] = pack8<DT>(s[2 * c2][nq], s[2 * c2 + 1][nq]);
+      for (int nq = 0; nq < NQ; ++nq) {
+        pb[c2][nq] = pack8<DT>(s[2 * c2][nq], s[2 * c2 + 1][nq]);
+      }
     }
   };
 
-  // `win` holds the page-table window of tiles kt+1 and kt+2 on entry to
-  // step kt and of tiles kt+2 and kt+3 on exit.
+  // Step kt: issue K and V of tile kt+2 into the buffers tile kt-1 used
+  // (every wave left tile kt-1 at the previous barrier); S(kt), mask if the
+  // tile needs it, softmax, O += V(kt)^T P(kt)^T; then wait for this wave's
+  // loads of tile kt+1 and barrier.  Tile t lives in buffer (t - first) % 3.
+  // `win` holds the page-table window of tile kt+2 on entry.
   int win;
-  // One tile: kc = K(kt), vp = V(kt-1), kw / vw receive K(kt+2) / V(kt+1).
-  auto step = [&](int kt, const char *kc, const char *vp, char *kw, char *vw) {
+  auto step = [&](int kt, const char *kc, const char *vc, char *kw, char *vw) __attribute__((always_inline)) {
     int issued = 0;
     if (kt + 2 <= kt_last) {
-      issue_k(win, kt + 1, kt + 2, kw);
-      issued += IPW;
+      issue_k(win, kt + 2, kt + 2, kw);
+      issue_v(win, kt + 2, kt + 2, vw);
+      issued = 2 * IPW;
     }
-    if (kt + 1 <= kt_last) {
-      issue_v(win, kt + 1, kt + 1, vw);
-      issued += IPW;
-    }
-    win = read_window(kt + 2);
+    win = read_window(kt + 3);
     compute_s(kc);
-    if (kt > kt_first) compute_pv(vp);
-#ifndef DD_PREFILL_MIDSYNC
-#define DD_PREFILL_MIDSYNC 0
-#endif
-    if (DD_PREFILL_MIDSYNC) sync(issued);
-    softmax(kt);
+    if (!tile_full(kt)) mask_s(kt);
+    softmax();
+    compute_pv(vc);
     sync(issued);
   };
 
-  // Prologue: K(first) alone, then K(first+1) and V(first) as if issued by
-  // the M phase of tile first-1.
+  // Prologue: tiles first and first+1.
   win = read_window(kt_first);
-  issue_k(win, kt_first, kt_first, s_k0);
   int issued = 0;
+  issue_k(win, kt_first, kt_first, s_k0);
+  issue_v(win, kt_first, kt_first, s_v0);
   if (kt_first + 1 <= kt_last) {
     issue_k(win, kt_first, kt_first + 1, s_k1);
-    issued += IPW;
+    issue_v(win, kt_first, kt_first + 1, s_v1);
+    issued = 2 * IPW;
   }
-  issue_v(win, kt_first, kt_first, s_v0);
-  issued += IPW;
   sync(issued);
-  win = read_window(kt_first + 1);
-  if (kPingPong && w >= 4) __syncthreads();  // second group: one phase behind
-
+  win = read_window(kt_first + 2);
   for (int kt = kt_first; kt <= kt_last; kt += 3) {
-    step(kt, s_k0, s_v2, s_k2, s_v1);
-    if (kt + 1 <= kt_last) step(kt + 1, s_k1, s_v0, s_k0, s_v2);
-    if (kt + 2 <= kt_last) step(kt + 2, s_k2, s_v1, s_k1, s_v0);
+    step(kt, s_k0, s_v0, s_k2, s_v2);
+    if (kt + 1 <= kt_last) step(kt + 1, s_k1, s_v1, s_k0, s_v0);
+    if (kt + 2 <= kt_last) step(kt + 2, s_k2, s_v2, s_k1, s_v1);
   }
-  // P.V of the last tile; its V was waited for before the last barrier.
-  switch ((kt_last - kt_first) % 3) {
-    case 0: compute_pv(s_v0); break;
-    case 1: compute_pv(s_v1); break;
-    default: compute_pv(s_v2); break;
-  }
-  if (kPingPong && w < 4) __syncthreads();  // same barrier count for both groups
 
   // ---- normalise and store: lane holds dims 16md + 4g4 + i of its column ----
   unsigned short *dst = (unsigned short *)p.out;
@@ -566,7 +533,13 @@ struct Geometry {
   int cols, kt;
 };
 constexpr Geometry kGeom64{16 * 2 * DD_PREFILL_NW, 64};
-constexpr Geometry kGeom128{16 * DD_PREFILL_NQ128 * DD_PREFILL_NW, 64};
+#ifndef DD_PREFILL_KT128
+#define DD_PREFILL_KT128 64
+#endif
+#ifndef DD_PREFILL_NW128
+#define DD_PREFILL_NW128 DD_PREFILL_NW
+#endif
+constexpr Geometry kGeom128{16 * DD_PREFILL_NQ128 * DD_PREFILL_NW128, DD_PREFILL_KT128};
 constexpr Geometry kGeom256{16 * 1 * DD_PREFILL_NW, 32};
 
 static bool geometry(int D, Geometry *g) {
@@ -582,7 +555,7 @@ template <int DT>
 int dispatch(const PrefillParams &p, int D, int max_len, int plan_len, hipStream_t s) {
   switch (D) {
     case 64: return launch<DT, 64, 2, kGeom64.kt, DD_PREFILL_NW>(p, max_len, plan_len, s);
-    case 128: return launch<DT, 128, DD_PREFILL_NQ128, kGeom128.kt, DD_PREFILL_NW>(p, max_len, plan_len, s);
+    case 128: return launch<DT, 128, DD_PREFILL_NQ128, kGeom128.kt, DD_PREFILL_NW128>(p, max_len, plan_len, s);
     case 256: return launch<DT, 256, 1, kGeom256.kt, DD_PREFILL_NW>(p, max_len, plan_len, s);
     default: return DD_EUNSUPPORTED;
   }
