@@ -266,7 +266,7 @@ __global__ __launch_bounds__(256) DD_DECODE_ATTR void decode_kernel(DecodeParams
     const char *vb = vbytes + KB * sb;
     if constexpr (KVT == DD_I8) {
 #pragma unroll
-      for (int c = 0; c < NC; ++c) R.k8[c] = *(const u32x2 *)(kb + (krow * D + 8 * r + 32 * c));
+      for (int c = 0; c < NC; ++c) R.k8[c] = __builtin_nontemporal_load((const u32x2 *)(kb + (krow * D + 8 * r + 32 * c)));
       const unsigned short *ksc = p.ks + (sb / D) * p.ngroups;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
@@ -274,15 +274,15 @@ __global__ __launch_bounds__(256) DD_DECODE_ATTR void decode_kernel(DecodeParams
       }
     } else if constexpr (kMfma) {
 #pragma unroll
-      for (int c = 0; c < NC; ++c) R.k[c] = *(const u32x4 *)(kb + 2u * (krow * D + 8 * r + 32 * c));
+      for (int c = 0; c < NC; ++c) R.k[c] = __builtin_nontemporal_load((const u32x4 *)(kb + 2u * (krow * D + 8 * r + 32 * c)));
     } else {
 #pragma unroll
-      for (int c = 0; c < NC4; ++c) R.k[c] = *(const u32x4 *)(kb + 4u * (krow * D + 4 * r + 16 * c));
+      for (int c = 0; c < NC4; ++c) R.k[c] = __builtin_nontemporal_load((const u32x4 *)(kb + 4u * (krow * D + 4 * r + 16 * c)));
     }
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
       const unsigned vrow = (unsigned)min(it * TPI + vtok_lane, lim);
-      R.v[it] = *(const u32x4 *)(vb + KB * (vrow * D + vdim));
+      R.v[it] = __builtin_nontemporal_load((const u32x4 *)(vb + KB * (vrow * D + vdim)));
       if constexpr (KVT == DD_I8) R.vs[it] = half_bits_to_float(p.vs[(sb / D) * p.ngroups + vrow * p.ngroups + vdim / p.group]);
     }
   };
