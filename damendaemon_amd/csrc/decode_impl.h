@@ -22,6 +22,8 @@
 //   * every wavefront keeps its own online softmax; the four are merged in
 //     LDS at the end of the split, and splits by a second small kernel.
 #pragma once
+#include <type_traits>
+
 #include "common.h"
 
 namespace dd_decode {
@@ -628,9 +630,31 @@ int dispatch_g(const DecodeParams &p, hipStream_t s, int phase) {
   return DD_EUNSUPPORTED;
 }
 
-// Instantiated once per dtype pair in decode_<dtype>.hip.
+}  // namespace dd_decode
+
+#include "decode_stream.h"
+
+namespace dd_decode {
+
+#ifndef DD_DECODE_STREAM
+#define DD_DECODE_STREAM 1
+#endif
+
+// Instantiated once per dtype pair in decode_<dtype>.hip.  bf16 / f16 pages
+// at D = 64, 128, 256 take the streamed kernel (decode_stream.h); fp32
+// pages, D = 96 and int8 pages take decode_kernel.
 template <int KVT, int QT>
 int dispatch_d(const DecodeParams &p, int D, hipStream_t s, int phase) {
+  if constexpr (DD_DECODE_STREAM && KVT == QT && (KVT == DD_BF16 || KVT == DD_F16)) {
+    if (p.G <= 16) {
+      switch (D) {
+        case 64: return launch_stream<KVT, 64, DD_STREAM_NB64, DD_STREAM_NW64>(p, s, phase);
+        case 128: return launch_stream<KVT, 128, DD_STREAM_NB128, DD_STREAM_NW128>(p, s, phase);
+        case 256: return launch_stream<KVT, 256, DD_STREAM_NB256, DD_STREAM_NW256>(p, s, phase);
+        default: break;
+      }
+    }
+  }
   switch (D) {
     case 64: return dispatch_g<KVT, QT, 64>(p, s, phase);
     case 96: return dispatch_g<KVT, QT, 96>(p, s, phase);
