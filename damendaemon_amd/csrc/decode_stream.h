@@ -117,6 +117,25 @@ DD_DEV u32x2 lds_read_tr16(unsigned addr) {
 #endif
   return r;
 }
+template <int OFF>
+DD_DEV u32x2 lds_read_b64(unsigned addr) {
+  u32x2 r = {};
+#if __HIP_DEVICE_COMPILE__
+  asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+#endif
+  return r;
+}
+// Transposing byte read (ds_read_b64_tr_b8): within each 16-lane group,
+// lane i receives byte i % 8 of the 8-byte chunks addressed by lanes
+// i / 8 + 2 j, j = 0..7, in that order.
+template <int OFF>
+DD_DEV u32x2 lds_read_tr8(unsigned addr) {
+  u32x2 r = {};
+#if __HIP_DEVICE_COMPILE__
+  asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+#endif
+  return r;
+}
 DD_DEV void wait_lds() {
 #if __HIP_DEVICE_COMPILE__
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -134,6 +153,64 @@ DD_DEV void wait_vm() {
 #if __HIP_DEVICE_COMPILE__
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 #endif
+}
+
+// Combine the waves of a workgroup and write the split's result: the
+// normalised output (one split) or the partial and its base-2 log-sum-exp.
+// `o` is this lane's O^T slice (head lane % 16, dims 16 md + 4 (lane / 16)
+// + i), `m_run` / `lsum` its head's running max and (lane-partial) sum.
+// `s_o` must hold NW * 16 * (D + 4) floats and be free (no loads in flight).
+template <int DT, int D, int NW>
+DD_DEV void stream_epilogue(const DecodeParams &p, float (*s_ml)[2][16], float *s_o, const f32x4 (&o)[D / 16],
+                            float m_run, float lsum, int w, int lane, int b, int kh, int split) {
+  constexpr int MD = D / 16;
+  constexpr int DP = D + 4;
+  const int n16 = lane & 15;
+  const int kg = lane >> 4;
+  const int G = p.G;
+  const long head0 = (long)b * p.H + (long)kh * G;
+  lsum = xor32_sum(xor16_sum(lsum));
+  if (lane < 16) {
+    s_ml[w][0][lane] = m_run;
+    s_ml[w][1][lane] = lsum;
+  }
+  __syncthreads();
+  float mm = s_ml[0][0][n16];
+#pragma unroll
+  for (int ww = 1; ww < NW; ++ww) mm = fmaxf(mm, s_ml[ww][0][n16]);
+  const float fac = m_run == kNegInf ? 0.f : fast_exp2(m_run - mm);
+  if (n16 < G) {
+#pragma unroll
+    for (int md = 0; md < MD; ++md) *(f32x4 *)&s_o[(w * 16 + n16) * DP + 16 * md + 4 * kg] = o[md] * fac;
+  }
+  __syncthreads();
+
+  for (int idx = threadIdx.x; idx < G * D; idx += 64 * NW) {
+    const int h = idx / D;
+    const int d = idx - h * D;
+    float m2 = s_ml[0][0][h];
+    for (int ww = 1; ww < NW; ++ww) m2 = fmaxf(m2, s_ml[ww][0][h]);
+    float l = 0.f, acc = 0.f;
+    for (int ww = 0; ww < NW; ++ww) {
+      const float mw = s_ml[ww][0][h];
+      if (mw != kNegInf) l += s_ml[ww][1][h] * fast_exp2(mw - m2);
+      acc += s_o[(ww * 16 + h) * DP + d];
+    }
+    const long bh = head0 + h;
+    if (p.splits == 1) {
+      if (p.sinks) {
+        const float sk = p.sinks[bh - (long)b * p.H] * kLog2e;
+        const float m3 = fmaxf(m2, sk);
+        const float f = fast_exp2(m2 - m3);
+        l = l * f + fast_exp2(sk - m3);
+        acc *= f;
+      }
+      store_as<DT>(p.out, bh * D + d, acc / l);
+    } else {
+      p.part[(bh * p.splits + split) * D + d] = acc / l;
+      if (d == 0) p.lse[bh * p.splits + split] = m2 + log2f(l);
+    }
+  }
 }
 
 template <int DT, int D, int NB, int NW>
@@ -229,9 +306,6 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
     const int pg = first + i * NW;
     long base;  // element offset of the chunk's first row, -1 when unmapped
     if (i >= n) {
-#ifdef DD_STREAM_NODUMMY
-      return;
-#endif
       base = -1;
     } else if (p.paged) {
       base = -1;
@@ -285,15 +359,6 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
     for (int md = 0; md < MD; ++md) after_wait(va[md]);
     // The stage is in registers now: refill it with chunk i + NB.
     issue(i + NB, decltype(stage_tag)::value);
-#ifdef DD_STREAM_NOMATH
-    {
-      unsigned x = 0;
-      for (int c = 0; c < NC; ++c) x ^= ka[c][0] ^ ka[c][3];
-      for (int md = 0; md < MD; ++md) x ^= va[md][0] ^ va[md][1];
-      lsum += (float)(x & 1);
-      return;
-    }
-#endif
 
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -376,56 +441,8 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
 #undef DD_STREAM_STEP
   }
   wait_vm<0>();  // the trailing (empty) loads, before the ring is reused
-#ifdef DD_STREAM_NOEPI
-  if (lsum == 12345.f) ((float *)p.out)[0] = lsum;
-  return;
-#endif
 
-  // ---- combine the four waves ---------------------------------------------
-  lsum = xor32_sum(xor16_sum(lsum));
-  if (lane < 16) {
-    s_ml[w][0][lane] = m_run;
-    s_ml[w][1][lane] = lsum;
-  }
-  __syncthreads();
-  float mm = s_ml[0][0][n16];
-#pragma unroll
-  for (int ww = 1; ww < NW; ++ww) mm = fmaxf(mm, s_ml[ww][0][n16]);
-  const float fac = m_run == kNegInf ? 0.f : fast_exp2(m_run - mm);
-  float *s_o = (float *)s_ring;
-  if (col_on) {
-#pragma unroll
-    for (int md = 0; md < MD; ++md)
-      *(f32x4 *)&s_o[(w * 16 + n16) * DP + 16 * md + 4 * kg] = o[md] * fac;
-  }
-  __syncthreads();
-
-  for (int idx = threadIdx.x; idx < G * D; idx += 64 * NW) {
-    const int h = idx / D;
-    const int d = idx - h * D;
-    float m2 = s_ml[0][0][h];
-    for (int ww = 1; ww < NW; ++ww) m2 = fmaxf(m2, s_ml[ww][0][h]);
-    float l = 0.f, acc = 0.f;
-    for (int ww = 0; ww < NW; ++ww) {
-      const float mw = s_ml[ww][0][h];
-      if (mw != kNegInf) l += s_ml[ww][1][h] * fast_exp2(mw - m2);
-      acc += s_o[(ww * 16 + h) * DP + d];
-    }
-    const long bh = head0 + h;
-    if (p.splits == 1) {
-      if (p.sinks) {
-        const float sk = p.sinks[bh - (long)b * p.H] * kLog2e;
-        const float m3 = fmaxf(m2, sk);
-        const float f = fast_exp2(m2 - m3);
-        l = l * f + fast_exp2(sk - m3);
-        acc *= f;
-      }
-      store_as<DT>(p.out, bh * D + d, acc / l);
-    } else {
-      p.part[(bh * p.splits + split) * D + d] = acc / l;
-      if (d == 0) p.lse[bh * p.splits + split] = m2 + log2f(l);
-    }
-  }
+  stream_epilogue<DT, D, NW>(p, s_ml, (float *)s_ring, o, m_run, lsum, w, lane, b, kh, split);
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
@@ -440,6 +457,366 @@ int launch_stream(const DecodeParams &p, hipStream_t stream, int phase) {
   }
   if ((phase & 2) && p.splits > 1) {
     hipLaunchKernelGGL((merge_kernel<DT>), dim3((unsigned)((long)p.B * p.H)), dim3(D < 256 ? D : 256), 0, stream,
+                       p, D);
+    DD_LAUNCH_CHECK();
+  }
+  return DD_OK;
+}
+
+
+// ---- int8 pages ------------------------------------------------------------
+//
+// Q8 pages (kv_quant.py:23-76 format: int8 rows + one fp16 scale per token,
+// KV head and `group` channels; NG = D / group scales per row, NG = 1 or
+// D / 32).  Same schedule as stream_kernel, but a wave consumes two 16-token
+// chunks (32 keys) at a time, so that P.V is one v_mfma_f32_16x16x32 per 16
+// dims: V^T comes from transposing byte reads (ds_read_b64_tr_b8), each lane
+// receiving 8 keys of one dim, widened exactly to bf16/f16 in registers;
+// K rows are read 8 bytes per lane and widened the same way.  Scales ride in
+// the same stage: K scales multiply the logits, V scales the probabilities.
+//
+// Stage layout: K rows of both chunks (32 x D bytes), V rows (32 x D), then
+// K scales and V scales of both chunks (4 x 32 NG bytes, room for NG = D/32).
+// Row R = 16 chunk + r stores its 8-byte column c at c ^ i8_swz(R): with it
+// the K reads (16 rows, 2 columns per half-wave) and the transposing V reads
+// (8 rows x 2 columns per half-wave) hit 32 distinct 8-byte bank slots.
+template <int D>
+DD_DEV constexpr int i8_swz(int R) {
+  const int hi = ((R >> 3) ^ (R >> 4)) & 1;
+  if constexpr (D == 64) {
+    return (((R >> 2) & 1) | (hi << 1)) << 1;
+  } else if constexpr (D == 128) {
+    return (((R >> 1) & 1) | (((R >> 2) & 1) << 1) | (hi << 2)) << 1;
+  } else {
+    return ((R & 1) | (((R >> 1) & 1) << 1) | (((R >> 2) & 1) << 2) | (hi << 3)) << 1;
+  }
+}
+
+template <int QT, int D, int NG, int NB, int NW>
+__global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
+#if __HIP_DEVICE_COMPILE__
+  constexpr int ROWB = D;               // bytes per token row
+  constexpr int CHB = 16 * ROWB;        // one 16-token chunk of K (or V)
+  constexpr int KOFF = 0, VOFF = 2 * CHB, SOFF0 = 4 * CHB;
+  constexpr int SCB = 32 * NG;          // scale bytes of one chunk (16 tokens x NG x 2)
+  constexpr int STAGE = 4 * CHB + 4 * D;  // scale room for NG up to D / 32
+  constexpr int IPC = CHB / 1024;       // 16-byte DMA instructions per chunk
+  constexpr int LPP = 4 * IPC + 4;      // loads per pair of chunks
+  constexpr int CPR16 = ROWB / 16;
+  constexpr int NC = D / 32;
+  constexpr int MD = D / 16;
+  constexpr int DP = D + 4;
+  static_assert(IPC >= 1 && LPP * NB < 64 && NB >= 2 && NB <= 4, "vmcnt range, unrolled steps");
+  static_assert(NG == 1 || NG == NC, "one scale per row or per 32 channels");
+  static_assert((NB - 1) * STAGE + SOFF0 + 4 * SCB < 65536, "ds offset range");
+  static_assert(NW * 16 * DP * 4 <= NW * NB * STAGE, "epilogue buffer fits the ring");
+
+  __shared__ __align__(1024) char s_ring[NW * NB * STAGE];
+  __shared__ float s_ml[NW][2][16];
+
+  const int lane = threadIdx.x & 63;
+  const int w = uniform(threadIdx.x >> 6);
+  const int n16 = lane & 15;
+  const int kg = lane >> 4;
+  const int G = p.G;
+
+  const int wg = blockIdx.x;
+  const int nbkh = p.B * p.KH;
+  const int split = wg / nbkh;
+  const int bkh = wg - split * nbkh;
+  const int b = bkh / p.KH;
+  const int kh = bkh - b * p.KH;
+
+  const long pos64 = p.pos[b];
+  const int row = p.slots ? (int)p.slots[b] : 0;
+  const int t_hi = pos64 + 1 < p.ctx_limit ? (int)pos64 + 1 : p.ctx_limit;
+  int t_lo = 0;
+  if (p.window > 0 && pos64 - p.window + 1 > 0) t_lo = (int)(pos64 - p.window + 1);
+  int s_lo = split * p.split_tokens;
+  int s_hi = s_lo + p.split_tokens;
+  if (s_hi > t_hi) s_hi = t_hi;
+  if (s_lo < t_lo) s_lo = t_lo;
+  if (s_lo >= s_hi) return;
+  const int pg_first = s_lo >> 4;
+  const int pg_last = (s_hi - 1) >> 4;
+  const long head0 = (long)b * p.H + (long)kh * G;
+  const bool col_on = n16 < G;
+
+  u32x4 qa[NC];
+  {
+    const unsigned short *qb = (const unsigned short *)p.q;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      qa[c] = col_on ? *(const u32x4 *)(qb + (head0 + n16) * D + 8 * kg + 32 * c) : u32x4{0, 0, 0, 0};
+  }
+  float slope = (p.alibi && col_on) ? p.alibi[(long)kh * G + n16] * kLog2e : 0.f;
+
+  const unsigned wbase = (unsigned)(size_t)(lds_void *)s_ring + (unsigned)(w * NB * STAGE);
+  // K operand: row n16 of chunk ch, 8-byte column 4c + kg.
+  unsigned k_addr[2][NC];
+#pragma unroll
+  for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int R = 16 * ch + n16;
+      k_addr[ch][c] = wbase + KOFF + R * ROWB + 8 * ((4 * c + kg) ^ i8_swz<D>(R));
+    }
+  // V^T operand: lane a of group kg addresses key slot j = a / 2 (chunk j / 4,
+  // row 4 kg + j % 4) and the 8 dims 16 md + 8 (a % 2).
+  unsigned v_addr[MD];
+  {
+    const int a = lane & 15;
+    const int j = a >> 1;
+    const int R = 16 * (j >> 2) + 4 * kg + (j & 3);
+#pragma unroll
+    for (int md = 0; md < MD; ++md) v_addr[md] = wbase + VOFF + R * ROWB + 8 * ((2 * md + (a & 1)) ^ i8_swz<D>(R));
+  }
+  // Scales of this lane's keys (rows 4kg .. 4kg+3 of each chunk).
+  const unsigned sc_addr = wbase + SOFF0 + 2 * (4 * kg * NG);
+
+  const int first = w;  // pair index; chunks pg_first + 2 pair, +1
+  const int npairs_all = (pg_last - pg_first) / 2 + 1;
+  const int n = first < npairs_all ? (npairs_all - 1 - first) / NW + 1 : 0;
+
+  const char *kplane = (const char *)p.k;
+  const char *vplane = (const char *)p.v;
+  const char *ksplane = (const char *)p.ks;
+  const char *vsplane = (const char *)p.vs;
+  const __attribute__((address_space(4))) int32_t *tab = (const __attribute__((address_space(4))) int32_t *)p.table;
+
+  // Element (= byte) offset of a chunk's first row, -1 when unmapped or dead.
+  auto chunk_row0 = [&](int pg, bool live_pair) __attribute__((always_inline)) -> long {
+    long base = -1;
+    if (!live_pair || pg > pg_last) return -1;
+    if (p.paged) {
+      if (row >= 0 && row < p.table_rows) {
+        const int entry = pg >> p.chunk_shift;
+        const long phys = tab[(long)row * p.table_w + entry];
+        if (phys >= 0 && phys < p.capacity)
+          base = ((phys * p.KH + kh) * (long)p.page + ((pg - (entry << p.chunk_shift)) << 4));
+      }
+    } else if (row >= 0 && row < p.capacity) {
+      base = ((long)row * p.KH + kh) * (long)p.page + (long)pg * 16;
+    }
+    return base;
+  };
+  auto issue = [&](int i, int stage) __attribute__((always_inline)) {
+    const int pair = first + i * NW;
+    char *dst = s_ring + (w * NB + stage) * STAGE;
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      const int pg = pg_first + 2 * pair + ch;
+      long base = chunk_row0(pg, i < n);
+      base = (long)uniform_ptr((const char *)base);
+      const int live = base < 0 ? 0 : max(0, min(16, s_hi - pg * 16));
+      const long rb = base < 0 ? 0 : base;  // token-row index
+      const int bytes = uniform(live * ROWB);
+      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)uniform_ptr(kplane + rb * ROWB), (short)0, bytes, kRawBufferWord3);
+      const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)uniform_ptr(vplane + rb * ROWB), (short)0, bytes, kRawBufferWord3);
+      const int sbytes = uniform(base < 0 ? 0 : SCB);
+      const __amdgpu_buffer_rsrc_t rks = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)uniform_ptr(ksplane + rb * 2 * NG), (short)0, sbytes, kRawBufferWord3);
+      const __amdgpu_buffer_rsrc_t rvs = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)uniform_ptr(vsplane + rb * 2 * NG), (short)0, sbytes, kRawBufferWord3);
+#pragma unroll
+      for (int j = 0; j < IPC; ++j) {
+        const int e = 64 * j + lane;
+        const int r = e / CPR16;
+        const int src16 = (e % CPR16) ^ (i8_swz<D>(16 * ch + r) >> 1);
+        const unsigned off = (unsigned)(r * ROWB + 16 * src16);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void *)(dst + KOFF + ch * CHB + 1024 * j), 16, off, 0,
+                                                 0, kStreamLoadAux);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void *)(dst + VOFF + ch * CHB + 1024 * j), 16, off, 0,
+                                                 0, kStreamLoadAux);
+      }
+      // SCB bytes each: only the first SCB / 4 lanes take part (an inactive
+      // lane writes nothing), so neighbouring scale blocks stay intact.
+      if (4 * lane < SCB) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rks, (lds_void *)(dst + SOFF0 + ch * SCB), 4, 4 * lane, 0, 0,
+                                                 kStreamLoadAux);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rvs, (lds_void *)(dst + SOFF0 + 2 * SCB + ch * SCB), 4, 4 * lane,
+                                                 0, 0, kStreamLoadAux);
+      }
+    }
+  };
+
+  f32x4 o[MD];
+#pragma unroll
+  for (int md = 0; md < MD; ++md) o[md] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegInf;
+  float lsum = 0.f;
+
+  auto consume = [&](int i, auto stage_tag) __attribute__((always_inline)) {
+    constexpr int SO = decltype(stage_tag)::value * STAGE;
+    const int t0 = (pg_first + 2 * (first + i * NW)) * 16;  // first key of the pair
+    u32x2 k8[2][NC];
+    u32x2 v8[MD];
+    u32x2 ks8[2][NG], vs8[2][NG];
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) k8[ch][c] = lds_read_b64<SO>(k_addr[ch][c]);
+#pragma unroll
+    for (int md = 0; md < MD; ++md) v8[md] = lds_read_tr8<SO>(v_addr[md]);
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        ks8[ch][g] = lds_read_b64<SO>(sc_addr + ch * SCB + 8 * g);
+        vs8[ch][g] = lds_read_b64<SO>(sc_addr + 2 * SCB + ch * SCB + 8 * g);
+      }
+    wait_lds();
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) after_wait(k8[ch][c]);
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        after_wait(ks8[ch][g]);
+        after_wait(vs8[ch][g]);
+      }
+    }
+#pragma unroll
+    for (int md = 0; md < MD; ++md) after_wait(v8[md]);
+    issue(i + NB, decltype(stage_tag)::value);
+
+    // scale of key 4kg + e of chunk ch, channel group g (fp16 at index e NG + g)
+    auto scale_of = [&](const u32x2 (&sc)[2][NG], int ch, int e, int g) __attribute__((always_inline)) {
+      const int idx = e * NG + g;
+      const unsigned wd = sc[ch][idx >> 2][(idx >> 1) & 1];
+      return half_bits_to_float((unsigned short)((idx & 1) ? (wd >> 16) : (wd & 0xffffu)));
+    };
+
+    // logits: s[ch][e] = key t0 + 16 ch + 4 kg + e for head n16
+    float x[2][4];
+    float mx = kNegInf;
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (NG == 1) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) sacc = mfma16x16x32<QT>(widen_i8x8<QT>(k8[ch][c]), qa[c], sacc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sacc[e] *= scale_of(ks8, ch, e, 0);
+      } else {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const f32x4 part = mfma16x16x32<QT>(widen_i8x8<QT>(k8[ch][c]), qa[c], f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sacc[e] += scale_of(ks8, ch, e, c) * part[e];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int t = t0 + 16 * ch + 4 * kg + e;
+        float v = sacc[e] * p.scale_log2 + slope * (float)t;
+        if (p.rel && col_on) {
+          const long dist = pos64 - t > 0 ? pos64 - t : 0;
+          v += p.rel[((long)kh * G + n16) * p.rel_buckets + rel_bucket((int)dist, p.rel_buckets, p.rel_denom)] *
+               kLog2e;
+        }
+        x[ch][e] = (t >= s_lo && t < s_hi) ? v : kNegInf;
+        mx = fmaxf(mx, x[ch][e]);
+      }
+    }
+    mx = xor32_max(xor16_max(mx));
+    const bool up = mx > m_run + kStreamSlack;
+    if (__builtin_amdgcn_ballot_w64(up)) {
+      const float mn = up ? mx : m_run;
+      const float alpha = up ? (m_run == kNegInf ? 0.f : fast_exp2(m_run - mn)) : 1.f;
+      m_run = mn;
+      lsum *= alpha;
+#pragma unroll
+      for (int md = 0; md < MD; ++md) o[md] *= alpha;
+    }
+    const float mu = m_run == kNegInf ? 0.f : m_run;
+    float pr[2][4];
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pr[ch][e] = fast_exp2(x[ch][e] - mu);
+        lsum += pr[ch][e];
+      }
+    // P^T operand per V scale group: slot j < 4 is key 4kg + j of chunk 0,
+    // slot j >= 4 key 4kg + j - 4 of chunk 1.  Dead keys have p = 0 and
+    // their (possibly garbage) scales are dropped.
+    u32x4 pb[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      float q[8];
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int t = t0 + 16 * ch + 4 * kg + e;
+          const float sc = (t >= s_lo && t < s_hi) ? scale_of(vs8, ch, e, g) : 0.f;
+          q[4 * ch + e] = pr[ch][e] * sc;
+        }
+      pb[g] = u32x4{pack_pair<QT>(q[0], q[1]), pack_pair<QT>(q[2], q[3]), pack_pair<QT>(q[4], q[5]),
+                    pack_pair<QT>(q[6], q[7])};
+    }
+    // Keys before the window start hold expired (possibly NaN) rows: zero
+    // their bytes in the V^T operand.  Byte j of a lane is key slot j.
+    if (t0 < s_lo) {
+      unsigned mlo = 0, mhi = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int t = t0 + 16 * (j >> 2) + 4 * kg + (j & 3);
+        if (t >= s_lo) {
+          if (j < 4) mlo |= 0xffu << (8 * j);
+          else mhi |= 0xffu << (8 * (j - 4));
+        }
+      }
+#pragma unroll
+      for (int md = 0; md < MD; ++md) v8[md] = u32x2{v8[md][0] & mlo, v8[md][1] & mhi};
+    }
+#pragma unroll
+    for (int md = 0; md < MD; ++md) {
+      const int g = NG == 1 ? 0 : (16 * md) / 32;
+      o[md] = mfma16x16x32<QT>(widen_i8x8<QT>(v8[md]), pb[g], o[md]);
+    }
+  };
+
+#pragma unroll
+  for (int u = 0; u < NB; ++u) issue(u, u);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) after_wait(qa[c]);
+  after_wait(slope);
+  for (int i0 = 0; i0 < n; i0 += NB) {
+#define DD_STREAM_STEP(U)                                                  \
+    if constexpr (U < NB) {                                                \
+      const int i = i0 + U;                                                \
+      if (i < n) {                                                         \
+        wait_vm<LPP * (NB - 1)>();                                         \
+        consume(i, std::integral_constant<int, (U < NB ? U : 0)>{});       \
+      }                                                                    \
+    }
+    DD_STREAM_STEP(0)
+    DD_STREAM_STEP(1)
+    DD_STREAM_STEP(2)
+    DD_STREAM_STEP(3)
+#undef DD_STREAM_STEP
+  }
+  wait_vm<0>();
+
+  stream_epilogue<QT, D, NW>(p, s_ml, (float *)s_ring, o, m_run, lsum, w, lane, b, kh, split);
+#endif  // __HIP_DEVICE_COMPILE__
+}
+
+template <int QT, int D, int NG, int NB, int NW>
+int launch_stream_i8(const DecodeParams &p, hipStream_t stream, int phase) {
+  const long grid = (long)p.B * p.KH * p.splits;
+  if (grid <= 0) return DD_OK;
+  if (grid > 0x7fffffffL) return DD_EINVAL;
+  if (phase & 1) {
+    hipLaunchKernelGGL((stream_i8_kernel<QT, D, NG, NB, NW>), dim3((unsigned)grid), dim3(64 * NW), 0, stream, p);
+    DD_LAUNCH_CHECK();
+  }
+  if ((phase & 2) && p.splits > 1) {
+    hipLaunchKernelGGL((merge_kernel<QT>), dim3((unsigned)((long)p.B * p.H)), dim3(D < 256 ? D : 256), 0, stream,
                        p, D);
     DD_LAUNCH_CHECK();
   }

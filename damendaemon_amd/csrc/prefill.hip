@@ -45,7 +45,10 @@ constexpr float kMaxSlack = 8.f;
 namespace {
 
 constexpr float kNegInf = -__builtin_inff();
-constexpr int kTabCache = 8192;  // page-table entries staged in LDS (128K keys at page 16)
+#ifndef DD_PREFILL_TAB
+#define DD_PREFILL_TAB 8192
+#endif
+constexpr int kTabCache = DD_PREFILL_TAB;  // page-table entries staged in LDS (128K keys at page 16)
 
 struct PrefillParams {
   const void *q;       // (T, H, D)
