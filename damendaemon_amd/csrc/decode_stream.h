@@ -742,11 +742,13 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
       }
     // P^T operand per V scale group: slot j < 4 is key 4kg + j of chunk 0,
     // slot j >= 4 key 4kg + j - 4 of chunk 1.  Dead keys have p = 0 and
-    // their (possibly garbage) scales are dropped.
-    u32x4 pb[NG];
+    // their (possibly garbage) scales are dropped.  p * scale is split into
+    // a high and a low 16-bit part (two MFMAs), so the fp16 scale keeps its
+    // full precision: with a single key the output is exactly int8 * scale.
+    u32x4 pb[NG], pl[NG];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      float q[8];
+      float q[8], r[8];
 #pragma unroll
       for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
@@ -757,6 +759,15 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
         }
       pb[g] = u32x4{pack_pair<QT>(q[0], q[1]), pack_pair<QT>(q[2], q[3]), pack_pair<QT>(q[4], q[5]),
                     pack_pair<QT>(q[6], q[7])};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const unsigned wd = pb[g][j >> 1];
+        const unsigned short hb = (unsigned short)((j & 1) ? (wd >> 16) : (wd & 0xffffu));
+        const float hi = QT == DD_BF16 ? __uint_as_float((unsigned)hb << 16) : half_bits_to_float(hb);
+        r[j] = q[j] - hi;
+      }
+      pl[g] = u32x4{pack_pair<QT>(r[0], r[1]), pack_pair<QT>(r[2], r[3]), pack_pair<QT>(r[4], r[5]),
+                    pack_pair<QT>(r[6], r[7])};
     }
     // Keys before the window start hold expired (possibly NaN) rows: zero
     // their bytes in the V^T operand.  Byte j of a lane is key slot j.
@@ -776,7 +787,8 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
 #pragma unroll
     for (int md = 0; md < MD; ++md) {
       const int g = NG == 1 ? 0 : (16 * md) / 32;
-      o[md] = mfma16x16x32<QT>(widen_i8x8<QT>(v8[md]), pb[g], o[md]);
+      const u32x4 vw = widen_i8x8<QT>(v8[md]);
+      o[md] = mfma16x16x32<QT>(vw, pl[g], mfma16x16x32<QT>(vw, pb[g], o[md]));
     }
   };
 

@@ -41,6 +41,11 @@ constexpr float kMaxSlack = 8.f;
 #ifndef DD_PREFILL_NQ128
 #define DD_PREFILL_NQ128 2
 #endif
+#ifndef DD_PREFILL_NBUF
+#define DD_PREFILL_NBUF 3
+#endif
+// K/V tiles in flight: a tile is issued NBUF - 1 steps before it is used.
+constexpr int NBUF = DD_PREFILL_NBUF;
 
 namespace {
 
@@ -163,14 +168,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
   static_assert(KBLK == VBLK && KBLK % NW == 0, "every wave issues whole blocks");
   constexpr int IPW = KBLK / NW;       // DMA instructions per wave per plane
   static_assert(NC % IPW == 0 && MD / 2 == NC, "a wave's blocks share one 16-key chunk");
-  static_assert(2 * IPW < 16, "vmcnt immediate");
+  static_assert(2 * (NBUF - 2) * IPW < 16, "vmcnt immediate");
 
   // Six distinct buffers (three K, three V).  Every direct-to-LDS load and
   // every LDS read below names one of them at compile time (the tile loop is
   // unrolled by three), so the compiler can tell that reads of one buffer do
   // not wait for loads still landing in another.
   __shared__ __align__(1024) char s_v0[PLANE], s_v1[PLANE], s_v2[PLANE];  // lowest addresses: read most
+  __shared__ __align__(1024) char s_v3[NBUF > 3 ? PLANE : 16];
   __shared__ __align__(16) char s_k0[PLANE], s_k1[PLANE], s_k2[PLANE];
+  __shared__ __align__(16) char s_k3[NBUF > 3 ? PLANE : 16];
   __shared__ int s_tab[kTabCache];                   // page-table window of this slot
 
   const int tid = threadIdx.x;
@@ -312,11 +319,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
   // Wait for every load of this wave except the `recent` issued last, then
   // barrier: all waves' older loads are visible and all waves have left the
   // phase before.
-  auto sync = [&](int recent) __attribute__((always_inline)) {
-    if (recent >= 2 * IPW) {
+  // Wait until only this wave's loads of the `younger` most recently issued
+  // tiles may still be in flight, then barrier: all waves' older loads are
+  // visible and all waves have left the phase before.
+  auto sync = [&](int younger) __attribute__((always_inline)) {
+    if (NBUF > 3 && younger >= 2) {
+      __builtin_amdgcn_s_waitcnt((NBUF > 3 ? 4 * IPW : 0) | (0x7 << 4) | (0xF << 8));
+    } else if (younger >= 1) {
       __builtin_amdgcn_s_waitcnt((2 * IPW) | (0x7 << 4) | (0xF << 8));
-    } else if (recent >= IPW) {
-      __builtin_amdgcn_s_waitcnt(IPW | (0x7 << 4) | (0xF << 8));
     } else {
       __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xF << 8));
     }
@@ -457,43 +467,51 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
     }
   };
 
-  // Step kt: issue K and V of tile kt+2 into the buffers tile kt-1 used
+  // Step kt: issue K and V of tile kt+NBUF-1 into the buffers tile kt-1 used
   // (every wave left tile kt-1 at the previous barrier); S(kt), mask if the
   // tile needs it, softmax, O += V(kt)^T P(kt)^T; then wait for this wave's
-  // loads of tile kt+1 and barrier.  Tile t lives in buffer (t - first) % 3.
-  // `win` holds the page-table window of tile kt+2 on entry.
+  // loads of tile kt+1 and barrier.  Tile t lives in buffer (t - first) %
+  // NBUF.  `win` holds the page-table window of tile kt+NBUF-1 on entry.
   int win;
   auto step = [&](int kt, const char *kc, const char *vc, char *kw, char *vw) __attribute__((always_inline)) {
-    int issued = 0;
-    if (kt + 2 <= kt_last) {
-      issue_k(win, kt + 2, kt + 2, kw);
-      issue_v(win, kt + 2, kt + 2, vw);
-      issued = 2 * IPW;
+    if (kt + NBUF - 1 <= kt_last) {
+      issue_k(win, kt + NBUF - 1, kt + NBUF - 1, kw);
+      issue_v(win, kt + NBUF - 1, kt + NBUF - 1, vw);
     }
-    win = read_window(kt + 3);
+    win = read_window(kt + NBUF);
     compute_s(kc);
     if (!tile_full(kt)) mask_s(kt);
     softmax();
     compute_pv(vc);
-    sync(issued);
+    sync(min(NBUF - 2, kt_last - kt - 1));
   };
 
-  // Prologue: tiles first and first+1.
+  // Prologue: tiles first .. first+NBUF-2.
   win = read_window(kt_first);
-  int issued = 0;
   issue_k(win, kt_first, kt_first, s_k0);
   issue_v(win, kt_first, kt_first, s_v0);
   if (kt_first + 1 <= kt_last) {
     issue_k(win, kt_first, kt_first + 1, s_k1);
     issue_v(win, kt_first, kt_first + 1, s_v1);
-    issued = 2 * IPW;
   }
-  sync(issued);
-  win = read_window(kt_first + 2);
-  for (int kt = kt_first; kt <= kt_last; kt += 3) {
-    step(kt, s_k0, s_v0, s_k2, s_v2);
-    if (kt + 1 <= kt_last) step(kt + 1, s_k1, s_v1, s_k0, s_v0);
-    if (kt + 2 <= kt_last) step(kt + 2, s_k2, s_v2, s_k1, s_v1);
+  if (NBUF > 3 && kt_first + 2 <= kt_last) {
+    win = read_window(kt_first + 2);
+    issue_k(win, kt_first + 2, kt_first + 2, s_k2);
+    issue_v(win, kt_first + 2, kt_first + 2, s_v2);
+  }
+  sync(min(NBUF - 2, kt_last - kt_first));
+  win = read_window(kt_first + NBUF - 1);
+  for (int kt = kt_first; kt <= kt_last; kt += NBUF) {
+    if constexpr (NBUF == 3) {
+      step(kt, s_k0, s_v0, s_k2, s_v2);
+      if (kt + 1 <= kt_last) step(kt + 1, s_k1, s_v1, s_k0, s_v0);
+      if (kt + 2 <= kt_last) step(kt + 2, s_k2, s_v2, s_k1, s_v1);
+    } else {
+      step(kt, s_k0, s_v0, s_k3, s_v3);
+      if (kt + 1 <= kt_last) step(kt + 1, s_k1, s_v1, s_k0, s_v0);
+      if (kt + 2 <= kt_last) step(kt + 2, s_k2, s_v2, s_k1, s_v1);
+      if (kt + 3 <= kt_last) step(kt + 3, s_k3, s_v3, s_k2, s_v2);
+    }
   }
 
   // ---- normalise and store: lane holds dims 16md + 4g4 + i of its column ----

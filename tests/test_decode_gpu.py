@@ -172,6 +172,31 @@ def test_int8_dim256_group32():
     check(run_case(case), oracle_case(case), torch.int8)
 
 
+@pytest.mark.parametrize('dim,group', [(64, 64), (64, 32), (128, 128), (128, 32), (256, 256)])
+@pytest.mark.parametrize('window', [0, 77])
+def test_int8_nan_scales_and_expired_rows(dim, group, window):
+    """Q8 pages whose unused rows (pool, page tails) and expired rows (before
+    the window) carry NaN scales and arbitrary bytes: none may be read."""
+    contexts = [1, 15, 17, 300, 1111, 2500]
+    case = paged_decode_case(contexts, 12, 3, dim, torch.float32, seed=dim + group + window, nan_fill=True)
+    qk, ks = oracle.quantize_q8(case['cache_k'], group)
+    qv, vs = oracle.quantize_q8(case['cache_v'], group)
+    expected = oracle.decode_attention(case['query'].to(torch.bfloat16), qk, qv, case['positions'], case['slots'],
+                                       page_table=case['page_table'], k_scale=ks, v_scale=vs, window=window)
+    ks[~torch.isfinite(ks)] = float('nan')
+    vs[~torch.isfinite(vs)] = float('nan')
+    if window:
+        for b, c in enumerate(contexts):
+            for t in range(max(0, c - window)):
+                page = int(case['page_table'][b, t // 16])
+                qk[page, :, t % 16] = 127
+                qv[page, :, t % 16] = -127
+                ks[page, :, t % 16] = float('nan')
+                vs[page, :, t % 16] = float('nan')
+    case.update(cache_k=qk, cache_v=qv, k_scale=ks, v_scale=vs, query=case['query'].to(torch.bfloat16))
+    check(run_case(case, window=window), expected, torch.int8)
+
+
 def test_alibi_sinks_relative_bias_with_splits():
     torch.manual_seed(3)
     case = paged_decode_case([3, 600, 2500, 5000], 8, 2, 128, torch.float16, seed=9)
