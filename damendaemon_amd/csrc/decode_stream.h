@@ -19,7 +19,8 @@
 // Math.  S^T = K Q^T with v_mfma_f32_16x16x32 (rows = the chunk's 16
 // tokens, columns = the GQA group's heads); the accumulator already has the
 // register layout of the P^T operand of O^T += V^T P^T, which runs on
-// v_mfma_f32_16x16x16 with V^T read from LDS by transposing reads
+// v_mfma_f32_16x16x16 (P^T split into a high and a residual 16-bit part, two
+// MFMAs, so p keeps ~17 bits) with V^T read from LDS by transposing reads
 // (ds_read_b64_tr_b16).  Each lane owns one head column, so the online
 // softmax needs only two permlane steps per chunk; the running max moves
 // only when a chunk's max exceeds it by more than 2^8 (p <= 256, exact in
@@ -396,7 +397,21 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
       pr[e] = fast_exp2(x[e] - mu);
       lsum += pr[e];
     }
+    // P^T in two 16-bit parts (high, and the residual): the P.V product
+    // then carries the fp32 probabilities to ~2^-17, as the reference's fp32
+    // weighted sum does, instead of the 2^-9 of one bf16 rounding.
     const u32x2 pb = {pack_pair<DT>(pr[0], pr[1]), pack_pair<DT>(pr[2], pr[3])};
+    u32x2 pl;
+    {
+      float r[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const unsigned wd = pb[e >> 1];
+        const unsigned short hb = (unsigned short)((e & 1) ? (wd >> 16) : (wd & 0xffffu));
+        r[e] = pr[e] - (DT == DD_BF16 ? __uint_as_float((unsigned)hb << 16) : half_bits_to_float(hb));
+      }
+      pl = u32x2{pack_pair<DT>(r[0], r[1]), pack_pair<DT>(r[2], r[3])};
+    }
 
     // Rows before the window start inside this chunk hold expired keys:
     // their V must not reach the MFMA (0 * NaN).
@@ -413,7 +428,7 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
       }
     }
 #pragma unroll
-    for (int md = 0; md < MD; ++md) o[md] = mfma16x16x16<DT>(va[md], pb, o[md]);
+    for (int md = 0; md < MD; ++md) o[md] = mfma16x16x16<DT>(va[md], pl, mfma16x16x16<DT>(va[md], pb, o[md]));
   };
 
   // Prologue: NB chunks in flight, then the query operand (loaded before

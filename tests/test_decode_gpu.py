@@ -197,6 +197,20 @@ def test_int8_nan_scales_and_expired_rows(dim, group, window):
     check(run_case(case, window=window), expected, torch.int8)
 
 
+@pytest.mark.parametrize('page', [32, 64])
+@pytest.mark.parametrize('kind', ['bf16', 'int8'])
+def test_larger_pages(page, kind):
+    """Pages of 32 / 64 tokens: a page holds several 16-token chunks."""
+    contexts = [3, 31, 32, 33, 700, 2049]
+    dtype = torch.bfloat16 if kind == 'bf16' else torch.float32
+    case = paged_decode_case(contexts, 16, 4, 128, dtype, seed=page, page=page, nan_fill=True)
+    if kind == 'int8':
+        qk, ks = oracle.quantize_q8(case['cache_k'], 128)
+        qv, vs = oracle.quantize_q8(case['cache_v'], 128)
+        case.update(cache_k=qk, cache_v=qv, k_scale=ks, v_scale=vs, query=case['query'].to(torch.bfloat16))
+    check(run_case(case), oracle_case(case), torch.bfloat16 if kind == 'bf16' else torch.int8)
+
+
 def test_alibi_sinks_relative_bias_with_splits():
     torch.manual_seed(3)
     case = paged_decode_case([3, 600, 2500, 5000], 8, 2, 128, torch.float16, seed=9)
