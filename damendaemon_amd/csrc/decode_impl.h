@@ -595,10 +595,23 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int D) {
   for (int s = s0; s <= s1; ++s) den += fast_exp2(lse[s] - mm);
   if (p.sinks) den += fast_exp2(sk - mm);
   const float inv = 1.f / den;
+  // Partials are read kBatch splits at a time with all loads in flight
+  // (a load-then-accumulate loop would expose one memory latency per split).
+  constexpr int kBatch = 8;
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
     float o = 0.f;
-    for (int s = s0; s <= s1; ++s) o += fast_exp2(lse[s] - mm) * inv * p.part[(bh * p.splits + s) * D + d];
-    store_as<QT>(p.out, bh * D + d, o);
+    for (int s = s0; s <= s1; s += kBatch) {
+      float v[kBatch], l[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const bool ok = s + j <= s1;
+        v[j] = ok ? p.part[(bh * p.splits + s + j) * D + d] : 0.f;
+        l[j] = ok ? lse[s + j] : -__builtin_inff();
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) o += fast_exp2(l[j] - mm) * v[j];
+    }
+    store_as<QT>(p.out, bh * D + d, o * inv);
   }
 }
 
