@@ -6,7 +6,8 @@ One step = one ragged paged decode attention over the whole batch
 a pool 1.25x the pages used), inputs resident in HBM before timing.
 
 Prints ONE JSON line (the driver's contract) with:
-  value        tokens/s = sequences per step / wall time per step
+  value        tokens/s = sequences per step / wall time per step, the step
+               (split kernel + merge) replayed from a captured HIP graph
   roofline     the split kernel (dominant) timed with HIP events on its own
                stream: algorithmic bytes per launch / its mean duration,
                against MI355X's 8 TB/s HBM3E peak
@@ -144,8 +145,9 @@ def main():
         launch.run()
     torch.cuda.synchronize()
 
+    # Kernel timing: the split kernel and the merge bracketed by HIP events on
+    # the launch stream (torch's current stream), K launches.
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    t0 = time.perf_counter()
     for e0, e1, e2 in events:
         e0.record()
         launch.partials()
@@ -153,9 +155,23 @@ def main():
         launch.merge()
         e2.record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
     split_ms = statistics.mean(e0.elapsed_time(e1) for e0, e1, _ in events)
     merge_ms = statistics.mean(e1.elapsed_time(e2) for _, e1, e2 in events)
+
+    # Throughput: the decode step captured once in a HIP graph and replayed,
+    # as the serving loop replays its captured decode (batch.py:25-46);
+    # W untimed replays, then exactly K timed ones between synchronisations.
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch.run()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
     ms_per_step = wall / args.steps * 1e3
     batch = case['query'].shape[0]
     achieved = nbytes / (split_ms * 1e-3) / 1e9
