@@ -23,7 +23,10 @@
 //     the register layout of the P^T operand (keys are contracted in a fixed
 //     permuted order that V^T is read in), and every lane owns one query
 //     column, so the online-softmax state needs no cross-lane shuffles
-//     beyond two xor-steps.
+//     beyond two xor-steps;
+//   * the softmax denominators come from the matrix cores too: one extra
+//     MFMA per P^T operand with an all-ones V^T yields the column sums of P
+//     (the P that the P.V product uses), so the VALU only exponentiates.
 #include "common.h"
 
 #include <algorithm>
@@ -256,12 +259,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
   }
 
   f32x4 o[MD][NQ];
-  float m_run[NQ], l_run[NQ], alpha[NQ];
+  float m_run[NQ], alpha[NQ];
+  // Row sums of P on the matrix cores: an all-ones V^T operand turns every
+  // accumulator row into sum_k P[k][column] (no VALU adds, no lane reduction).
+  f32x4 lacc[NQ];
+  const unsigned one2 = DT == DD_BF16 ? 0x3F803F80u : 0x3C003C00u;
+  const u32x4 ones = {one2, one2, one2, one2};
   bool grew = false;
 #pragma unroll
   for (int nq = 0; nq < NQ; ++nq) {
     m_run[nq] = kNegInf;
-    l_run[nq] = 0.f;
+    lacc[nq] = f32x4{0.f, 0.f, 0.f, 0.f};
     alpha[nq] = 1.f;
 #pragma unroll
     for (int md = 0; md < MD; ++md) o[md][nq] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -365,7 +373,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
       for (int nq = 0; nq < NQ; ++nq) {
 #pragma unroll
         for (int md = 0; md < MD; ++md) o[md][nq] *= alpha[nq];
+        lacc[nq] *= alpha[nq];
       }
+    }
+#pragma unroll
+    for (int c2 = 0; c2 < C2; ++c2) {
+#pragma unroll
+      for (int nq = 0; nq < NQ; ++nq) lacc[nq] = mfma<DT>(ones, pb[c2][nq], lacc[nq]);
     }
     // V^T operand of (md, c2): half h of key chunk c2 lives in block pair
     // (2c2 + h, md/2); the operand of the next md is read while the MFMAs of
@@ -446,17 +460,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
       const float mu = mn == kNegInf ? 0.f : mn * sc;
       alpha[nq] = up ? __builtin_amdgcn_exp2f(m_run[nq] * sc - mu) : 1.f;
       m_run[nq] = mn;
-      float ls = 0.f;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[mt][nq][i], sc, -mu));
           s[mt][nq][i] = e;
-          ls += e;
         }
       }
-      l_run[nq] = l_run[nq] * alpha[nq] + ls;
     }
 #pragma unroll
     for (int c2 = 0; c2 < C2; ++c2) {
@@ -518,8 +529,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
   unsigned short *dst = (unsigned short *)p.out;
 #pragma unroll
   for (int nq = 0; nq < NQ; ++nq) {
-    float l = l_run[nq];
-    l = xor32_sum(xor16_sum(l));
+    const float l = lacc[nq][0];
     if (!colok[nq]) continue;
     const float inv = 1.f / l;
     const int c = w * 16 * NQ + nq * 16 + l16;
