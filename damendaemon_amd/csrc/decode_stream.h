@@ -368,15 +368,20 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
     // logits of tokens t0 + 4kg + i for head n16
     float x[4];
     float mx = kNegInf;
+    float rb[4] = {0.f, 0.f, 0.f, 0.f};
+    if (p.rel) {  // workgroup-uniform: no per-lane branch in the common path
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int t = t0 + 4 * kg + e;
+        const long dist = pos64 - t > 0 ? pos64 - t : 0;
+        rb[e] = p.rel[((long)kh * G + (col_on ? n16 : 0)) * p.rel_buckets +
+                      rel_bucket((int)dist, p.rel_buckets, p.rel_denom)] * kLog2e;
+      }
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int t = t0 + 4 * kg + e;
-      float v = s[e] * p.scale_log2 + slope * (float)t;
-      if (p.rel && col_on) {
-        const long dist = pos64 - t > 0 ? pos64 - t : 0;
-        v += p.rel[((long)kh * G + n16) * p.rel_buckets + rel_bucket((int)dist, p.rel_buckets, p.rel_denom)] *
-             kLog2e;
-      }
+      const float v = s[e] * p.scale_log2 + slope * (float)t + rb[e];
       x[e] = (t >= s_lo && t < s_hi) ? v : kNegInf;
       mx = fmaxf(mx, x[e]);
     }
@@ -723,15 +728,20 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
           for (int e = 0; e < 4; ++e) sacc[e] += scale_of(ks8, ch, e, c) * part[e];
         }
       }
+      float rb[4] = {0.f, 0.f, 0.f, 0.f};
+      if (p.rel) {  // workgroup-uniform
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int t = t0 + 16 * ch + 4 * kg + e;
+          const long dist = pos64 - t > 0 ? pos64 - t : 0;
+          rb[e] = p.rel[((long)kh * G + (col_on ? n16 : 0)) * p.rel_buckets +
+                        rel_bucket((int)dist, p.rel_buckets, p.rel_denom)] * kLog2e;
+        }
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int t = t0 + 16 * ch + 4 * kg + e;
-        float v = sacc[e] * p.scale_log2 + slope * (float)t;
-        if (p.rel && col_on) {
-          const long dist = pos64 - t > 0 ? pos64 - t : 0;
-          v += p.rel[((long)kh * G + n16) * p.rel_buckets + rel_bucket((int)dist, p.rel_buckets, p.rel_denom)] *
-               kLog2e;
-        }
+        const float v = sacc[e] * p.scale_log2 + slope * (float)t + rb[e];
         x[ch][e] = (t >= s_lo && t < s_hi) ? v : kNegInf;
         mx = fmaxf(mx, x[ch][e]);
       }
