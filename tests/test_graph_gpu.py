@@ -1,0 +1,38 @@
+"""Decode attention captured in a HIP graph (the reference captures its decode
+step, damendaemon/batch.py:25-46): every replay must reproduce the eager
+result bit for bit, with eager work and synchronisations between replays."""
+import pytest
+import torch
+
+from damendaemon_amd import kernels
+from damendaemon_amd.workloads import paged_decode_case
+
+pytestmark = pytest.mark.gpu
+DEV = 'cuda'
+
+
+@pytest.mark.parametrize('kind', ['bf16', 'int8'])
+def test_decode_graph_replays_match_eager(kind):
+    case = paged_decode_case([17, 600, 2500, 4097, 9000], 32, 8, 128, torch.bfloat16, seed=31)
+    d = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    ks = vs = None
+    if kind == 'int8':
+        from damendaemon_amd import kv_quant
+        ck, ks = kv_quant.quantize_kv(d['cache_k'], group=128)
+        cv, vs = kv_quant.quantize_kv(d['cache_v'], group=128)
+        d['cache_k'], d['cache_v'] = ck, cv
+    launch = kernels.prepare_attention(d['query'], d['cache_k'], d['cache_v'], d['positions'], d['slots'],
+                                       page_table=d['page_table'], k_scale=ks, v_scale=vs)
+    assert launch.splits > 1
+    eager = launch.run().clone()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch.run()
+    for i in range(3):
+        launch.out.fill_(float('nan'))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(launch.out, eager), f'replay {i} differs from the eager launch'
+        torch.randn(1024, device=DEV).sum().item()  # unrelated eager work between replays
