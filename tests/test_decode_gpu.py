@@ -224,6 +224,24 @@ def test_alibi_sinks_relative_bias_with_splits():
         check(run_case(case, **dev_kw), oracle_case(case, **kw), torch.float16)
 
 
+@pytest.mark.parametrize('group', [32, 128])
+def test_int8_alibi_sinks_relative_bias(group):
+    """The bias, sink and window terms on the int8 path (two chunks per step)."""
+    torch.manual_seed(5)
+    case = paged_decode_case([3, 600, 2500, 5000], 8, 2, 128, torch.float32, seed=19)
+    qk, ks = oracle.quantize_q8(case['cache_k'], group)
+    qv, vs = oracle.quantize_q8(case['cache_v'], group)
+    case.update(cache_k=qk, cache_v=qv, k_scale=ks, v_scale=vs, query=case['query'].to(torch.bfloat16))
+    heads = 8
+    alibi = torch.linspace(-0.01, -0.001, heads)
+    sinks = torch.randn(heads)
+    rel = torch.randn(heads, 32)
+    for kw in ({'alibi': alibi, 'sinks': sinks, 'window': 300},
+               {'relative_bias': rel, 'relative_max_distance': 128}):
+        dev_kw = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in kw.items()}
+        check(run_case(case, **dev_kw), oracle_case(case, **kw), torch.int8)
+
+
 def test_sinks_single_split():
     case = paged_decode_case([3, 60, 100], 4, 2, 64, torch.float16, seed=4)
     sinks = torch.tensor([0.5, -1.0, 2.0, 0.0])
