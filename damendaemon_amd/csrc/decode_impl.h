@@ -45,6 +45,7 @@ struct DecodeParams {
   const float *sinks;
   long capacity;  // pages (paged) or slots (slotted); guards addressing
   int B, H, KH, G;
+  int gsub;       // workgroups per (sequence, KV head): query heads in groups of <= 16
   int table_w, table_rows;
   int page;       // page_size (paged) or context (slotted)
   int ctx_limit;  // table_w * page (paged) or context (slotted)
@@ -175,17 +176,22 @@ __global__ __launch_bounds__(256) DD_DECODE_ATTR void decode_kernel(DecodeParams
   const int w = uniform(threadIdx.x >> 6);
   const int r = lane >> 4;
   const int tl = lane & 15;
-  const int G = p.G;
 
   // Split-major order: every sequence's first split is dispatched before any
   // second split, so full-length splits run first and the short (or empty)
-  // final splits fill the tail of the launch.
+  // final splits fill the tail of the launch.  With more than 16 query heads
+  // per KV head, (sequence, KV head) is covered by gsub workgroups of up to
+  // 16 heads each.
   const int wg = blockIdx.x;
-  const int nbkh = p.B * p.KH;
+  const int per_b = p.KH * p.gsub;
+  const int nbkh = p.B * per_b;
   const int split = wg / nbkh;
   const int bkh = wg - split * nbkh;
-  const int b = bkh / p.KH;
-  const int kh = bkh % p.KH;
+  const int b = bkh / per_b;
+  const int vk = bkh - b * per_b;
+  const int kh = vk / p.gsub;
+  const int sub = vk - kh * p.gsub;
+  const int G = p.gsub > 1 ? min(GB, p.G - sub * GB) : p.G;
 
   const long pos64 = p.pos[b];
   const int row = p.slots ? (int)p.slots[b] : 0;
@@ -200,7 +206,7 @@ __global__ __launch_bounds__(256) DD_DECODE_ATTR void decode_kernel(DecodeParams
 
   const int pg_first = s_lo >> 4;
   const int pg_last = (s_hi - 1) >> 4;
-  const long head0 = (long)b * p.H + (long)kh * G;
+  const long head0 = (long)b * p.H + (long)kh * p.G + (long)sub * GB;
 
   // ---- query operand ----------------------------------------------------
   u32x4 qa[kMfma ? NC : 1];
@@ -618,7 +624,7 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int D) {
 // phase bit 1: split kernel; bit 2: merge kernel (only when splits > 1).
 template <int KVT, int QT, int D, int GB>
 int launch_decode(const DecodeParams &p, hipStream_t stream, int phase) {
-  const long grid = (long)p.B * p.KH * p.splits;
+  const long grid = (long)p.B * p.KH * p.gsub * p.splits;
   if (grid <= 0) return DD_OK;
   if (grid > 0x7fffffffL) return DD_EINVAL;
   if (phase & 1) {
@@ -640,7 +646,9 @@ int dispatch_g(const DecodeParams &p, hipStream_t s, int phase) {
   if (p.G <= 4) return launch_decode<KVT, QT, D, 4>(p, s, phase);
   if (p.G <= 8) return launch_decode<KVT, QT, D, 8>(p, s, phase);
   if (p.G <= 16) return launch_decode<KVT, QT, D, 16>(p, s, phase);
-  return DD_EUNSUPPORTED;
+  DecodeParams wide = p;
+  wide.gsub = (p.G + 15) / 16;
+  return launch_decode<KVT, QT, D, 16>(wide, s, phase);
 }
 
 }  // namespace dd_decode

@@ -24,10 +24,15 @@
 //     permuted order that V^T is read in), and every lane owns one query
 //     column, so the online-softmax state needs no cross-lane shuffles
 //     beyond two xor-steps;
-//   * the softmax denominators come from the matrix cores too: one extra
-//     MFMA per P^T operand with an all-ones V^T yields the column sums of P
-//     (the P that the P.V product uses), so the VALU only exponentiates.
+//   * P^T enters the P.V product as two 16-bit operands, its rounded high
+//     part and the rounded residual, so the probabilities keep ~17 bits as
+//     in the reference's fp32 softmax (one bf16 rounding, 2^-9 relative,
+//     puts short-context rows several 1e-3 off);
+//   * the softmax denominators come from the matrix cores too: extra MFMAs
+//     of the same two P^T operands with an all-ones V^T yield the column
+//     sums of exactly the P the P.V product uses.
 #include "common.h"
+#include "prefill_generic.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -74,7 +79,8 @@ struct PrefillParams {
   int page, page_shift;
   int table_w, table_rows;
   int window;
-  float scale_log2;
+  float scale_log2;     // |scale| * log2(e)
+  unsigned q_sign;      // 0x80008000 when scale < 0: q enters negated (exact), so logits use |scale|
 };
 
 template <int DT>
@@ -119,6 +125,27 @@ DD_DEV u32x4 pack8(f32x4 x0, f32x4 x1) {
     r[3] = __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{x1[2], x1[3]}, f16x2));
   }
   return r;
+}
+
+// The residuals x - hi(x) of eight probabilities whose 16-bit high parts
+// are `hi` (pack8 of the same x0, x1), as one more 8 x 16-bit operand: the
+// P.V product with hi and with this residual carries P to ~2^-17 relative,
+// where one 16-bit rounding would leave 2^-9 (bf16) or 2^-12 (fp16).
+template <int DT>
+DD_DEV float hi_part(unsigned w, int half) {
+  if constexpr (DT == DD_BF16) {
+    return half ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
+  } else {
+    return half ? f16_hi(w) : f16_lo(w);
+  }
+}
+template <int DT>
+DD_DEV u32x4 residual8(f32x4 x0, f32x4 x1, u32x4 hi) {
+  const f32x4 r0 = {x0[0] - hi_part<DT>(hi[0], 0), x0[1] - hi_part<DT>(hi[0], 1), x0[2] - hi_part<DT>(hi[1], 0),
+                    x0[3] - hi_part<DT>(hi[1], 1)};
+  const f32x4 r1 = {x1[0] - hi_part<DT>(hi[2], 0), x1[1] - hi_part<DT>(hi[2], 1), x1[2] - hi_part<DT>(hi[3], 0),
+                    x1[3] - hi_part<DT>(hi[3], 1)};
+  return pack8<DT>(r0, r1);
 }
 
 template <int DT>
@@ -225,19 +252,19 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
   const int kt_first = k_lo / KT;
   const int kt_last = (k_hi - 1) / KT;
 
-  // The page-table entries of the whole key range are staged in LDS once,
-  // already validated (-1 for an unallocated entry or one outside the cache),
-  // so no global page-table load or bounds test sits on a tile's critical path.
+  // The page-table entries of the key range are staged in LDS once, already
+  // validated (-1 for an unallocated entry or one outside the cache), so no
+  // global page-table load or bounds test sits on a tile's critical path.
+  // Entries past the first kTabCache of a very long history are read from
+  // the table itself when their tile comes up.
   const int e_first = (kt_first * KT) >> p.page_shift;
   const int e_count = ((((kt_last + 1) * KT) - 1) >> p.page_shift) - e_first + 1;
-  {
-    const bool slot_ok = slot >= 0 && slot < p.table_rows;
-    for (int i = tid; i < e_count && i < kTabCache; i += NT) {
-      const int e = e_first + i;
-      const int phys = (slot_ok && e < p.table_w) ? p.table[slot * p.table_w + e] : -1;
-      s_tab[i] = (phys >= 0 && phys < p.capacity) ? phys : -1;
-    }
-  }
+  const bool slot_ok = slot >= 0 && slot < p.table_rows;
+  auto table_entry = [&](int e) {
+    const int phys = (slot_ok && e < p.table_w) ? p.table[slot * p.table_w + e] : -1;
+    return (phys >= 0 && phys < p.capacity) ? phys : -1;
+  };
+  for (int i = tid; i < e_count && i < kTabCache; i += NT) s_tab[i] = table_entry(e_first + i);
 
   // ---- per-lane query columns and Q^T operands ----
   int qpos[NQ];
@@ -254,7 +281,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
     const long row = (tok0 + r0 + (colok[nq] ? r : 0)) * p.H + (long)kh * G + gh;
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc) {
-      qb[nq][cc] = colok[nq] ? *(const u32x4 *)(qsrc + row * D + 8 * g4 + 32 * cc) : u32x4{0, 0, 0, 0};
+      qb[nq][cc] = colok[nq] ? *(const u32x4 *)(qsrc + row * D + 8 * g4 + 32 * cc) ^ p.q_sign : u32x4{0, 0, 0, 0};
     }
   }
 
@@ -283,7 +310,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
   // v_readlane instead of a dependent LDS round trip each.
   auto read_window = [&](int kt) -> int {
     const int i = ((kt * KT) >> p.page_shift) - e_first + lane;
-    return s_tab[i < kTabCache ? i : kTabCache - 1];
+    if (i < kTabCache) return s_tab[i];
+    return i < e_count ? table_entry(e_first + i) : -1;
   };
   const int my_chunk = (w * IPW) / NC;   // every K and V block this wave loads lies in it
   const unsigned k_lane = 2u * (l16 * D + 8 * g4);             // K block, + 64cc bytes
@@ -364,7 +392,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
   // 32c2 + 16 + 4g4 + (j - 4): exactly the keys this lane's S^T registers
   // of chunks 2c2 and 2c2+1 hold, and the keys the two transposing reads
   // below return for rows 32c2 + 4g4 + (l16/4) and 16 further on.
-  u32x4 pb[C2][NQ];
+  u32x4 pb[C2][NQ], pl[C2][NQ];  // P^T high parts and residuals
   auto compute_pv = [&](const char *vt_lds) __attribute__((always_inline)) {
     // O is rescaled only when some column's running max moved in the
     // softmax that produced P (rare after the first tile); wave-uniform.
@@ -379,7 +407,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
 #pragma unroll
     for (int c2 = 0; c2 < C2; ++c2) {
 #pragma unroll
-      for (int nq = 0; nq < NQ; ++nq) lacc[nq] = mfma<DT>(ones, pb[c2][nq], lacc[nq]);
+      for (int nq = 0; nq < NQ; ++nq) lacc[nq] = mfma<DT>(ones, pl[c2][nq], mfma<DT>(ones, pb[c2][nq], lacc[nq]));
     }
     // V^T operand of (md, c2): half h of key chunk c2 lives in block pair
     // (2c2 + h, md/2); the operand of the next md is read while the MFMAs of
@@ -402,7 +430,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
 #pragma unroll
       for (int c2 = 0; c2 < C2; ++c2) {
 #pragma unroll
-        for (int nq = 0; nq < NQ; ++nq) o[md][nq] = mfma<DT>(va[c2], pb[c2][nq], o[md][nq]);
+        for (int nq = 0; nq < NQ; ++nq) o[md][nq] = mfma<DT>(va[c2], pl[c2][nq], mfma<DT>(va[c2], pb[c2][nq], o[md][nq]));
       }
       if (md + 1 < MD) {
 #pragma unroll
@@ -415,7 +443,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
   // A tile below every column's diagonal (and inside every window) needs no
   // mask; the test is workgroup-uniform.  Columns past the segment keep
   // finite logits and are never stored.  The running max is kept on raw
-  // logits (scale > 0) and only moved when a tile's max exceeds it by more
+  // logits (the kernel's scale is positive: a negative one negates q) and only moved when a tile's max exceeds it by more
   // than kMaxSlack in the exp2 domain.
   const float sc = p.scale_log2;
   const float slack = kMaxSlack / sc;
@@ -474,6 +502,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
 #pragma unroll
       for (int nq = 0; nq < NQ; ++nq) {
         pb[c2][nq] = pack8<DT>(s[2 * c2][nq], s[2 * c2 + 1][nq]);
+        pl[c2][nq] = residual8<DT>(s[2 * c2][nq], s[2 * c2 + 1][nq], pb[c2][nq]);
       }
     }
   };
@@ -603,9 +632,11 @@ extern "C" int dd_prefill_attention(const void *q, const void *k, const void *v,
   if (!q || !k || !v || !cu_seqlens || !context_lens || !slots || !page_table || !out || n < 0 || max_len < 0 ||
       heads <= 0 || kv_heads <= 0 || heads % kv_heads || page_size <= 0 || capacity <= 0 || table_width <= 0)
     return DD_EINVAL;
-  if (heads / kv_heads > 16) return DD_EUNSUPPORTED;
-  if ((long)max_context > (long)kTabCache * page_size) return DD_EUNSUPPORTED;
+  (void)max_context;  // any history length: page-table entries past the LDS cache come from global memory
   if (plan && plan_len <= 0) return DD_EINVAL;
+  // softmax(q.k * scale): a zero or non-finite scale has no max-tracking
+  // online form here (masked keys would meet 0 * inf)
+  if (!(scale != 0.f && __builtin_isfinite(scale))) return DD_EINVAL;
   if (n == 0 || max_len == 0) return DD_OK;
   PrefillParams p{};
   p.q = q;
@@ -629,8 +660,35 @@ extern "C" int dd_prefill_attention(const void *q, const void *k, const void *v,
   p.table_w = table_width;
   p.table_rows = table_rows;
   p.window = window > 0 ? window : 0;
-  p.scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
+  Geometry geom;
+  if (dtype == DD_F32 || !geometry(dim, &geom)) {
+    // fp32 pages and other head sizes: the vector-ALU kernel (no plan)
+    PrefillGenericArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.cu = cu_seqlens;
+    a.ctx = context_lens;
+    a.slots = slots;
+    a.table = page_table;
+    a.out = out;
+    a.capacity = capacity;
+    a.n = n;
+    a.max_len = max_len;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.dim = dim;
+    a.page = page_size;
+    a.page_shift = p.page_shift;
+    a.table_w = table_width;
+    a.table_rows = table_rows;
+    a.window = p.window;
+    a.scale_log2 = scale * kLog2e;
+    return dd_prefill_generic(a, dtype, s);
+  }
+  p.scale_log2 = __builtin_fabsf(scale) * kLog2e;
+  p.q_sign = scale < 0.f ? 0x80008000u : 0u;
   if (dtype == DD_BF16) return dispatch<DD_BF16>(p, dim, max_len, plan_len, s);
   if (dtype == DD_F16) return dispatch<DD_F16>(p, dim, max_len, plan_len, s);
   return DD_EUNSUPPORTED;

@@ -10,6 +10,7 @@ run of single-token segments by the split-KV decode kernel.  Both read the
 pages directly; nothing is gathered.
 """
 import ctypes
+import math
 
 import numpy as np
 import torch
@@ -24,8 +25,8 @@ def _check(query, cache_k, cache_v, page_table):
     T, H, D = query.shape
     capacity, KH, page, kd = cache_k.shape
     if (kd != D or cache_v.shape != cache_k.shape or H % KH or cache_k.dtype != query.dtype
-            or cache_v.dtype != query.dtype or query.dtype not in (torch.bfloat16, torch.float16)):
-        raise ValueError('prefill attention needs bf16/fp16 query and pages of one dtype and head size')
+            or cache_v.dtype != query.dtype or query.dtype not in (torch.bfloat16, torch.float16, torch.float32)):
+        raise ValueError('prefill attention needs bf16/fp16/fp32 query and pages of one dtype and head size')
     if not (query.is_contiguous() and cache_k.is_contiguous() and cache_v.is_contiguous()):
         raise ValueError('prefill attention needs contiguous tensors')
     if page_table.dtype != torch.int32 or page_table.ndim != 2 or not page_table.is_contiguous():
@@ -67,23 +68,35 @@ def prefill_attention(query, cache_k, cache_v, packed, page_table, window=0, sca
     """
     q = _check(query, cache_k, cache_v, page_table)
     T, H, D = q.shape
-    out = torch.empty_like(q) if out is None else out.reshape(q.shape)
+    scale = float(D ** -.5 if scale is None else scale)
+    if not math.isfinite(scale) or scale == 0.0:
+        raise ValueError('prefill attention needs a finite, non-zero scale')
+    if out is None:
+        out = torch.empty_like(q)
+    else:
+        if (out.dtype != q.dtype or out.device != q.device or out.numel() != q.numel()
+                or not out.is_contiguous()):
+            raise ValueError('out must be a contiguous tensor of the query dtype, device and size')
+        out = out.view(q.shape)
     a, b = segments if segments is not None else (0, len(packed.lengths))
     if b <= a:
         return out
     max_len = max(packed.lengths[a:b])
     max_context = max(s + n for s, n in zip(packed.starts[a:b], packed.lengths[a:b]))
-    if max_context > 8192 * cache_k.shape[2]:
-        raise ValueError('prefill attention supports up to 8192 pages of history per segment')
-    plan = prefill_plan(packed.lengths[a:b], packed.starts[a:b], H, cache_k.shape[1], D, window)
-    if len(plan) == 0:
-        return out
-    plan_dev = torch.from_numpy(plan).pin_memory().to(q.device, non_blocking=True)
+    plan_dev, plan_len = None, 0
+    if q.dtype != torch.float32 and D in (64, 128, 256):
+        # the MFMA kernel's XCD-balanced workgroup order (the fp32 / other-D
+        # kernel takes none)
+        plan = prefill_plan(packed.lengths[a:b], packed.starts[a:b], H, cache_k.shape[1], D, window)
+        if len(plan) == 0:
+            return out
+        plan_dev = torch.from_numpy(plan).pin_memory().to(q.device, non_blocking=True)
+        plan_len = len(plan)
     call('dd_prefill_attention', ptr(q), ptr(cache_k), ptr(cache_v), DTYPE_CODES[q.dtype],
          ptr(packed.cu_seqlens[a:]), ptr(packed.context_lens[a:]), ptr(packed._meta[2, a:]), b - a, max_len, max_context,
          ptr(page_table), page_table.shape[0], page_table.shape[1], H, cache_k.shape[1], D, cache_k.shape[2],
-         cache_k.shape[0], int(window or 0), float(D ** -.5 if scale is None else scale),
-         ptr(plan_dev), len(plan), ptr(out), _native.stream_of(q))
+         cache_k.shape[0], int(window or 0), scale,
+         ptr(plan_dev) if plan_dev is not None else None, plan_len, ptr(out), _native.stream_of(q))
     return out
 
 

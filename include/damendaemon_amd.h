@@ -218,12 +218,16 @@ int dd_rope_batch(const void *qkv, int qkv_dtype, const void *cos,
  * Chunked-prefill attention over the paged cache (the attention half of
  * damendaemon/paged.py:97-111: copy_pages gather + lower-right causal SDPA
  * of qwen2.py:754-770), without materialising the gathered K/V.
- *   q, out        (T, heads, dim) packed query / output rows, bf16 or fp16
+ *   q, out        (T, heads, dim) packed query / output rows, bf16, fp16 or
+ *                 fp32 (fp32, and head sizes other than 64/128/256 up to 256
+ *                 in steps of 4, take a vector-ALU kernel; bf16/fp16 at
+ *                 64/128/256 the MFMA kernel)
  *   k, v          (capacity, kv_heads, page_size, dim) pages holding every
  *                 segment's history including the chunk itself
  *   cu_seqlens    int64 (n+1), context_lens int64 (n) = start+len, slots int64 (n)
  *   max_len       the longest segment (sizes the grid)
- *   max_context   the longest start+len; at most 8192 pages per segment
+ *   max_context   the longest start+len (informational; any length)
+ *   scale         any finite non-zero value (0 or non-finite: DD_EINVAL)
  *   plan          NULL, or the device copy of dd_prefill_plan's output for
  *                 these same lengths/starts (plan_len entries): the
  *                 workgroup order; NULL uses a fixed XCD-aware order
