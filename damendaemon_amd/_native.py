@@ -16,7 +16,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 LIBRARY = Path(__file__).resolve().parent / '_lib' / 'libdamendaemon_amd.so'
 
 F32, F16, BF16, I8 = 0, 1, 2, 3
@@ -50,6 +50,8 @@ SIGNATURES['dd_prefill_indices'] = [_i64, _i, _i, _i64, _i64, _p, _p]
 SIGNATURES['dd_ring_decode_indices'] = [_p, _i64, _i, _i, _i, _p, _p]
 SIGNATURES['dd_decode_partials'] = SIGNATURES['dd_decode_attention']
 SIGNATURES['dd_decode_merge'] = SIGNATURES['dd_decode_attention']
+# the allocation-free variant: no partial / lse arguments
+SIGNATURES['dd_decode_attention_static'] = SIGNATURES['dd_decode_attention'][:-5] + [_i, _i, _p]
 
 
 class NativeError(RuntimeError):

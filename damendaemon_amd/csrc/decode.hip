@@ -2,6 +2,8 @@
 // dtype pair in decode_<dtype>.hip so the library compiles in parallel.
 #include "decode_impl.h"
 
+#include <mutex>
+
 using namespace dd_decode;
 
 extern template int dd_decode::dispatch_d<DD_BF16, DD_BF16>(const DecodeParams &, int, hipStream_t, int);
@@ -119,4 +121,66 @@ extern "C" int dd_decode_merge(const void *q, int q_dtype, const void *k, const 
                                    int rel_buckets, float rel_denom, const float *sinks, void *out,
                                    float *partial, float *lse, int splits, int split_tokens, void *stream) {
   return decode_entry(2, q, q_dtype, k, v, kv_dtype, k_scale, v_scale, group, positions, slots, page_table, table_rows, table_width, batch, heads, kv_heads, dim, page_size, capacity, window, scale, alibi, rel_bias, rel_buckets, rel_denom, sinks, out, partial, lse, splits, split_tokens, stream);
+}
+
+// ---- allocation-free variant ----------------------------------------------
+// The split partials and log-sum-exps live in this file-scope device array
+// instead of caller buffers.  Each GPU the library runs on holds its own copy
+// (DD_STATIC_SCRATCH_FLOATS fp32, 32 MiB) until the process ends.  Every
+// call on a GPU shares that GPU's copy: calls that overlap on one GPU (two
+// streams, or two threads) race.  No element needs clearing between calls:
+// the merge reads only the splits that the split kernel of the same call
+// wrote for each (sequence, head).
+static __device__ __align__(256) float scratch[DD_STATIC_SCRATCH_FLOATS];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float *g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device, set once
+
+// Device address of this GPU's `scratch`, looked up on the first call on
+// each device with that device current (the array's host-side name is not a
+// device address).  nullptr on failure.
+float *static_scratch(hipStream_t stream) {
+  int dev = -1;
+  if (hipStreamGetDevice(stream, &dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev]) return g_scratch_ptr[dev];
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+  if (cur != dev && hipSetDevice(dev) != hipSuccess) return nullptr;
+  void *addr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+  if (cur != dev) (void)hipSetDevice(cur);
+  if (e != hipSuccess || !addr) return nullptr;
+  g_scratch_ptr[dev] = (float *)addr;
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" int dd_decode_attention_static(const void *q, int q_dtype, const void *k, const void *v, int kv_dtype,
+                                          const void *k_scale, const void *v_scale, int group,
+                                          const int64_t *positions, const int64_t *slots,
+                                          const int32_t *page_table, int table_rows, int table_width, int batch,
+                                          int heads, int kv_heads, int dim, int page_size, int64_t capacity,
+                                          int window, float scale, const float *alibi, const float *rel_bias,
+                                          int rel_buckets, float rel_denom, const float *sinks, void *out,
+                                          int splits, int split_tokens, void *stream) {
+  if (batch < 0 || heads <= 0 || dim <= 0 || splits <= 0) return DD_EINVAL;
+  // partials (batch*heads, splits, dim) then lse (batch*heads, splits)
+  const long rows = (long)batch * heads * splits;
+  const long need = rows * (dim + 1L);
+  if (splits > 1 && need > (long)DD_STATIC_SCRATCH_FLOATS) return DD_ESCRATCH;
+  float *part = nullptr, *lse = nullptr;
+  if (splits > 1 && batch > 0) {
+    float *base = static_scratch((hipStream_t)stream);
+    if (!base) return DD_ELAUNCH;
+    part = base;
+    lse = base + rows * dim;
+  }
+  return decode_entry(3, q, q_dtype, k, v, kv_dtype, k_scale, v_scale, group, positions, slots, page_table,
+                      table_rows, table_width, batch, heads, kv_heads, dim, page_size, capacity, window, scale,
+                      alibi, rel_bias, rel_buckets, rel_denom, sinks, out, part, lse, splits, split_tokens, stream);
 }

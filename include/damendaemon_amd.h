@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define DD_ABI_VERSION 2
+#define DD_ABI_VERSION 3
 
 enum dd_dtype { DD_F32 = 0, DD_F16 = 1, DD_BF16 = 2, DD_I8 = 3 };
 
@@ -126,6 +126,31 @@ int dd_decode_merge(const void *q, int q_dtype, const void *k, const void *v,
                     int rel_buckets, float rel_denom, const float *sinks,
                     void *out, float *partial, float *lse, int splits,
                     int split_tokens, void *stream);
+
+/*
+ * dd_decode_attention without the partial / lse arguments, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  The split scratch is a file-scope device array of
+ * DD_STATIC_SCRATCH_FLOATS fp32 per GPU (32 MiB), held until the process
+ * ends; batch*heads*splits*(dim+1) must fit in it (else DD_ESCRATCH, e.g.
+ * at dim 128 about 65k (sequence, head, split) rows).  Calls share that
+ * array per GPU: calls that overlap on one GPU race.  Allocates nothing.
+ */
+#define DD_STATIC_SCRATCH_FLOATS (8 * 1024 * 1024)
+int dd_decode_attention_static(const void *q, int q_dtype, const void *k,
+                               const void *v, int kv_dtype,
+                               const void *k_scale, const void *v_scale,
+                               int group, const int64_t *positions,
+                               const int64_t *slots,
+                               const int32_t *page_table, int table_rows,
+                               int table_width, int batch, int heads,
+                               int kv_heads, int dim, int page_size,
+                               int64_t capacity, int window, float scale,
+                               const float *alibi, const float *rel_bias,
+                               int rel_buckets, float rel_denom,
+                               const float *sinks, void *out, int splits,
+                               int split_tokens, void *stream);
 
 /*
  * Q8_0 KV codec (damendaemon/kv_quant.py:48-76), bit-exact with the
