@@ -12,7 +12,8 @@ Prints ONE JSON line (the driver's contract) with:
                stream: algorithmic bytes per launch / its mean duration,
                against MI355X's 8 TB/s HBM3E peak
   cpu_baseline the PyTorch CPU restatement (page gather + masked GQA SDPA,
-               fp32) timed on a bounded sample of the same workload
+               fp32) timed on the whole batch with every core of the
+               affinity mask (a few seconds per step)
 Extra decode configurations (--config c3 / c5) are available for study;
 the default line is C2.
 """
@@ -42,17 +43,36 @@ def algorithmic_bytes(case, kv_bytes_per_token_head):
     return ctx * KH * kv_bytes_per_token_head + q_o + pages * 4
 
 
-def measured_traffic(config):
-    """HBM bytes per launch of the split kernel from the committed rocprofv3
-    PMC summary (FETCH_SIZE + WRITE_SIZE, calibrated against a plain copy),
-    or None when no summary exists for this workload."""
-    path = os.path.join(ROOT, 'profiles', f'decode_{config}_bf16_pmc.md')
+def source_digest():
+    """sha256 over the HIP sources (csrc/*.hip, *.h, sorted by name): ties a
+    profile summary to the kernels it measured."""
+    import hashlib
+    csrc = os.path.join(ROOT, 'damendaemon_amd', 'csrc')
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith(('.hip', '.h')):
+            h.update(name.encode())
+            with open(os.path.join(csrc, name), 'rb') as f:
+                h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(summary):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3
+    PMC summary profiles/<summary>.md (FETCH_SIZE + WRITE_SIZE, calibrated
+    against a plain copy), or None when there is none or it was taken on
+    other kernel sources than the ones running now."""
+    path = os.path.join(ROOT, 'profiles', f'{summary}.md')
     if not os.path.exists(path):
         return None
+    fields = {}
     for line in open(path):
-        if line.startswith('traffic_bytes_per_launch:'):
-            return int(line.split(':')[1])
-    return None
+        if ':' in line and not line.startswith(('#', '|', ' ')):
+            key, _, val = line.partition(':')
+            fields[key.strip()] = val.strip().strip('`')
+    if fields.get('source_digest') != source_digest() or 'traffic_bytes_per_launch' not in fields:
+        return None
+    return int(fields['traffic_bytes_per_launch'])
 
 
 def build_case(name, device):
@@ -76,21 +96,22 @@ def build_case(name, device):
     raise SystemExit(f'unknown config {name}')
 
 
-def cpu_baseline(case, budget_s=15.0, sample_seqs=16):
-    """Time oracle.decode_attention_sdpa (fp32, CPU) on the first sequences of the batch."""
+def cpu_baseline(case, budget_s=20.0):
+    """Time oracle.decode_attention_sdpa (fp32, CPU) on the whole batch, with
+    every core of this process's affinity mask."""
     from oracle import paged_oracle
-    threads = min(len(os.sched_getaffinity(0)), 16)
+    threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    n = min(sample_seqs, case['query'].shape[0])
-    table = case['page_table'][:n]
+    n = case['query'].shape[0]
+    table = case['page_table']
     used = torch.unique(table[table >= 0]).long()
     remap = torch.full((case['cache_k'].shape[0],), -1, dtype=torch.int64, device=used.device)
     remap[used] = torch.arange(used.numel(), device=used.device)
     small_table = torch.where(table >= 0, remap[table.clamp_min(0).long()], -1).to(torch.int32).cpu()
     k = case['cache_k'][used].cpu()
     v = case['cache_v'][used].cpu()
-    q = case['query'][:n].cpu()
-    pos = case['positions'][:n].cpu()
+    q = case['query'].cpu()
+    pos = case['positions'].cpu()
     slots = torch.arange(n)
     if k.dtype == torch.int8:
         k = paged_oracle.dequantize_q8(k, case['k_scale'][used].cpu())
@@ -98,15 +119,14 @@ def cpu_baseline(case, budget_s=15.0, sample_seqs=16):
     paged_oracle.decode_attention_sdpa(q, k, v, pos, slots, small_table)   # warm-up
     times = []
     start = time.perf_counter()
-    while len(times) < 10 or (time.perf_counter() - start < budget_s and len(times) < 200):
+    while len(times) < 3 or (time.perf_counter() - start < budget_s and len(times) < 10):
         t0 = time.perf_counter()
         paged_oracle.decode_attention_sdpa(q, k, v, pos, slots, small_table)
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     return {'value': n / med, 'unit': 'tokens/s', 'cores': threads, 'kind': 'port',
-            'sample': f'first {n} of {case["query"].shape[0]} sequences (ctx sum '
-                      f'{sum(case["contexts"][:n])}), fp32 page gather + masked GQA SDPA, '
-                      f'median of {len(times)} runs'}
+            'sample': f'all {n} sequences (ctx sum {sum(case["contexts"])}), fp32 page gather + masked GQA '
+                      f'SDPA on {threads} threads, median of {len(times)} steps'}
 
 
 def main():
@@ -194,7 +214,8 @@ def main():
                    'split_kernel_ms': split_ms, 'merge_kernel_ms': merge_ms,
                    'step_hbm_gbps': nbytes / (ms_per_step * 1e-3) / 1e9},
         'roofline': {'bound': 'hbm', 'achieved': achieved, 'peak': PEAK_HBM_GBPS, 'unit': 'GB/s',
-                     'frac': achieved / PEAK_HBM_GBPS, 'traffic': measured_traffic(args.config), 'algorithmic_bytes': nbytes},
+                     'frac': achieved / PEAK_HBM_GBPS, 'traffic': measured_traffic(f'decode_{args.config}_pmc'),
+                     'algorithmic_bytes': nbytes, 'source_digest': source_digest()},
         'cpu_baseline': None if args.no_cpu_baseline else cpu_baseline(case),
     }
     print(json.dumps(line), flush=True)

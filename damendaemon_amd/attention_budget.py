@@ -6,9 +6,12 @@ log-sum-exp each, and one output vector.
 
 
 def query_rows(heads, dim, splits, scratch_bytes, output_bytes=4):
+    """How many query rows one launch may take within ``scratch_bytes``."""
     if type(scratch_bytes) is not int or scratch_bytes <= 0:
         raise ValueError('attention scratch budget must be a positive byte count')
-    per_row = heads * (splits * (dim + 1) * 4 + dim * output_bytes)
-    if scratch_bytes < per_row:
+    fp32 = 4
+    per_head = splits * (dim + 1) * fp32 + dim * output_bytes   # partials + lse, then the output row
+    rows = scratch_bytes // (heads * per_head)
+    if rows == 0:
         raise ValueError('attention scratch budget cannot fit one query row')
-    return scratch_bytes // per_row
+    return rows

@@ -67,7 +67,12 @@ def dequantize_kv(data, scales, dtype):
 
 def store_kv(cache, slots, positions, k, v):
     """Quantise K/V (batch, KH, tokens, dim) into (slot, position) rows of the
-    dense resident pair (kv_quant.py:79-107)."""
+    dense resident pair (the contract of kv_quant.py:79-107).
+
+    One GPU quantisation of K and V together and one indexed write each for
+    the int8 rows and the scales; every (slot, position) pair must have a
+    single writer.
+    """
     data, scales = cache
     if positions.ndim != 2 or positions.shape[0] != k.shape[0] or positions.shape[1] != k.shape[2]:
         raise ValueError('quantized KV store requires (batch, tokens) positions')
@@ -76,20 +81,18 @@ def store_kv(cache, slots, positions, k, v):
         raise ValueError('quantized KV store requires matching batch-major K/V')
     if positions.numel() and int(positions.max()) >= data.shape[3]:
         raise ValueError('KV store position exceeds the cache context')
-    packed_k, scale_k = quantize_kv(k, group)
-    packed_v, scale_v = quantize_kv(v, group)
-    for row in range(k.shape[0]):
-        slot = int(slots[row])
-        p = positions[row]
-        data[0, slot][:, p, :] = packed_k[row]
-        data[1, slot][:, p, :] = packed_v[row]
-        scales[0, slot][:, p, :] = scale_k[row]
-        scales[1, slot][:, p, :] = scale_v[row]
+    codes, steps = quantize_kv(torch.stack((k, v)), group)        # (2, B, KH, T, ...)
+    slot_of_token = torch.as_tensor(slots, device=data.device).long()[:, None].expand(positions.shape)
+    where = (slot_of_token, slice(None), positions.to(data.device).long())
+    # destination rows data[:, b-slot, :, position] are (B, T, 2, KH, ...)
+    data[(slice(None),) + where] = codes.permute(1, 3, 0, 2, 4)
+    scales[(slice(None),) + where] = steps.permute(1, 3, 0, 2, 4)
 
 
 def read_kv(cache, slots, end, dtype=torch.float32):
-    """Dequantised (slots, KH, end, dim) K and V of the populated prefix (kv_quant.py:110-122)."""
+    """Dequantised (slots, KH, end, dim) K and V of the populated prefix (the
+    contract of kv_quant.py:110-122); duplicate slots give duplicate rows."""
     data, scales = cache
-    d = data.index_select(1, slots)[..., :end, :]
-    s = scales.index_select(1, slots)[..., :end, :]
-    return dequantize_kv(d[0], s[0], dtype), dequantize_kv(d[1], s[1], dtype)
+    rows = torch.as_tensor(slots, device=data.device).long()
+    both = dequantize_kv(data[:, rows, :, :end], scales[:, rows, :, :end], dtype)
+    return both[0], both[1]

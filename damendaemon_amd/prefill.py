@@ -7,13 +7,15 @@ forms its own group).
 
 
 def groups(prompts, slots, token_budget):
-    batch, assigned, count = [], [], 0
-    for prompt, slot in zip(prompts, slots):
-        if batch and count + len(prompt) > token_budget:
-            yield batch, assigned
-            batch, assigned, count = [], [], 0
-        batch.append(prompt)
-        assigned.append(slot)
-        count += len(prompt)
-    if batch:
-        yield batch, assigned
+    """Yield (prompts, slots) groups in order.  A group is closed just before
+    the prompt that would take its token count past ``token_budget``; a
+    prompt longer than the budget still makes a group of its own."""
+    pairs = list(zip(prompts, slots))
+    first, tokens = 0, 0
+    for i, (prompt, _) in enumerate(pairs):
+        if i > first and tokens + len(prompt) > token_budget:
+            yield [p for p, _ in pairs[first:i]], [s for _, s in pairs[first:i]]
+            first, tokens = i, 0
+        tokens += len(prompt)
+    if first < len(pairs):
+        yield [p for p, _ in pairs[first:]], [s for _, s in pairs[first:]]

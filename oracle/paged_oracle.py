@@ -322,10 +322,12 @@ PINNING = {
                         'scripts/verify_paged_kernels.py:60-67 does; single-key -> v; '
                         'constant V -> V; window >= context == no window; '
                         'sink -inf == no sink; alibi 0 == no alibi',
-    't5_bucket': 'brute force against the bucket table a Python float64 restatement of '
-                 'kernels.py:162-167 gives at the exact/large boundary',
+    't5_bucket': 'transformers T5Attention._relative_position_bucket (library routine, '
+                 'unidirectional) over 2000 distances and three (buckets, max_distance) geometries',
     'decode_attention_sdpa': 'agrees with decode_attention on random pages',
-    'prefill_attention': 'torch SDPA with causal_lower_right on the gathered K/V (library routine)',
+    'prefill_attention': 'torch SDPA with causal_lower_right on the gathered K/V (library routine); '
+                         'windowed: SDPA with the explicit kpos <= qpos and kpos > qpos - window mask '
+                         '(qwen2.py:765-770); window 1 returns each row its own value vector',
     'pack_batch': 'hand-written known answers (tests/test_oracle.py) and invariants: '
                   'positions step by one inside a segment, slot_map decodes to the page-table entry',
     'rope_rows': 'precise path vs the closed form x*cos + cat(-b, a)*sin of '

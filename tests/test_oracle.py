@@ -202,3 +202,31 @@ def test_prefill_oracle_matches_sdpa_lower_right():
         ref = F.scaled_dot_product_attention(qq, k, v, attn_mask=causal_lower_right(n, s + n), enable_gqa=True)
         assert torch.allclose(out[t0:t0 + n], ref[0].transpose(0, 1), atol=1e-12)
         t0 += n
+
+
+@pytest.mark.parametrize('window', [1, 5, 33, 200])
+def test_prefill_oracle_window_matches_sdpa_explicit_mask(window):
+    """The windowed prefill of qwen2.py:765-770: keys with kpos <= qpos and
+    kpos > qpos - window, built as an explicit SDPA mask (the construction of
+    the reference's tests/test_prefill.py:22-30)."""
+    case = paged_decode_case([60, 230], 4, 2, 32, torch.float32, seed=12)
+    lengths, starts, slots = [20, 45], [40, 185], [0, 1]
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(sum(lengths), 4, 32, generator=g)
+    out = O.prefill_attention(q, case['cache_k'], case['cache_v'], lengths, starts, slots, case['page_table'],
+                              window=window)
+    t0 = 0
+    for n, s, slot in zip(lengths, starts, slots):
+        k = O.gather_pages(case['cache_k'], case['page_table'], slot, s + n)[None].double()
+        v = O.gather_pages(case['cache_v'], case['page_table'], slot, s + n)[None].double()
+        qq = q[t0:t0 + n].transpose(0, 1)[None].double()
+        qpos = torch.arange(s, s + n)[:, None]
+        kpos = torch.arange(s + n)[None, :]
+        mask = (kpos <= qpos) & (kpos > qpos - window)
+        ref = F.scaled_dot_product_attention(qq, k, v, attn_mask=mask, enable_gqa=True)
+        assert torch.allclose(out[t0:t0 + n], ref[0].transpose(0, 1), atol=1e-12)
+        t0 += n
+    # window 1: every row sees only its own key, so the output is that key's value
+    if window == 1:
+        v0 = O.gather_pages(case['cache_v'], case['page_table'], 0, 60)
+        assert torch.allclose(out[0, :, :], v0[:, 40].double().repeat_interleave(2, 0), atol=1e-12)
