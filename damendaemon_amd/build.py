@@ -23,8 +23,13 @@ FLAGS = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}',
          '-Wno-unused-command-line-argument']
 
 
+# Per-source flags.  prefill32.hip: MFMAs in their VGPR form, so that the
+# S^T accumulators the softmax reads are not shuttled through AGPRs.
+SOURCE_FLAGS = {'prefill32.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form=1']}
+
+
 def _compile(source, obj, extra=()):
-    cmd = [HIPCC, *FLAGS, *extra, '-c', str(source), '-o', str(obj)]
+    cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(source.name, []), *extra, '-c', str(source), '-o', str(obj)]
     run = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = '\n'.join(l for l in run.stderr.splitlines() if noise not in l)
