@@ -23,9 +23,8 @@ FLAGS = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}',
          '-Wno-unused-command-line-argument']
 
 
-# Per-source flags.  prefill32.hip: MFMAs in their VGPR form, so that the
-# S^T accumulators the softmax reads are not shuttled through AGPRs.
-SOURCE_FLAGS = {'prefill32.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form=1']}
+# Per-source extra flags (none at present).
+SOURCE_FLAGS = {}
 
 
 def _compile(source, obj, extra=()):

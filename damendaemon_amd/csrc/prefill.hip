@@ -10,8 +10,8 @@
 // reference gathers start+len tokens with copy_pages before its SDPA.
 //
 // This file holds the C entry point, the host-side workgroup plan, and the
-// 16x16x32 MFMA kernel used for head size 256 (prefill32.hip takes 64 and
-// 128, prefill_generic.hip fp32 pages and other head sizes).
+// 16x16x32 MFMA kernel used for head size 256 (prefill_pipe.hip takes 64
+// and 128, prefill_generic.hip fp32 pages and other head sizes).
 //
 // MI355X design of the 16x16x32 kernel:
 //   * a workgroup owns one KV head and 16*NQ*NW (query row, head) columns of
@@ -485,8 +485,8 @@ int launch(PrefillParams p, int max_len, int plan_len, hipStream_t s) {
 struct Geometry {
   int cols, kt;
 };
-constexpr Geometry kGeom64{128, 32};   // prefill32_kernel: 4 waves x 32 columns, 32-key tiles
-constexpr Geometry kGeom128{128, 32};
+constexpr Geometry kGeom64{256, 64};   // prefill_pipe_kernel: 8 waves x 32 columns, 64-key tiles
+constexpr Geometry kGeom128{256, 64};
 constexpr Geometry kGeom256{16 * 1 * DD_PREFILL_NW, 32};
 
 static bool geometry(int D, Geometry *g) {
@@ -502,7 +502,7 @@ template <int DT>
 int dispatch(const PrefillParams &p, int D, int max_len, int plan_len, hipStream_t s) {
   switch (D) {
     case 64:
-    case 128: return prefill32_dispatch(p, DT, D, max_len, plan_len, s);
+    case 128: return prefill_pipe_dispatch(p, DT, D, max_len, plan_len, s);
     case 256: return launch<DT, 256, 1, kGeom256.kt, DD_PREFILL_NW>(p, max_len, plan_len, s);
     default: return DD_EUNSUPPORTED;
   }

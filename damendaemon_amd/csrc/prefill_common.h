@@ -1,5 +1,5 @@
 // Shared pieces of the chunked-prefill MFMA kernels (prefill.hip,
-// prefill32.hip): the launch parameters, MFMA wrappers, 16-bit operand
+// prefill_pipe.hip): the launch parameters, MFMA wrappers, 16-bit operand
 // packing of the probabilities and the transposing LDS read.
 #pragma once
 
@@ -132,6 +132,6 @@ constexpr int kBufferWord3 = 0x00020000;
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-int prefill32_dispatch(const PrefillParams &p, int dtype, int dim, int max_len, int plan_len, hipStream_t s);
+int prefill_pipe_dispatch(const PrefillParams &p, int dtype, int dim, int max_len, int plan_len, hipStream_t s);
 
 }  // namespace dd_prefill

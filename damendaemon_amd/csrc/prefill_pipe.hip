@@ -1,0 +1,540 @@
+// Chunked-prefill attention for head sizes 64 and 128 (gfx950), bf16 or
+// fp16 pages; semantics as in prefill.hip (damendaemon/paged.py:97-111 with
+// qwen2.py:754-770): query row j of segment i attends keys 0 .. start_i + j
+// of its slot (and > position - window), GQA head h reads KV head h / G,
+// softmax(q.k * scale) . v accumulated in fp32.
+//
+// Work split.  A workgroup of eight waves (two per SIMD, one workgroup per
+// CU) owns 256 (query row, head) columns of one (segment, KV head), 32 per
+// wave; keys stream in 64-key tiles (four 16-token chunks).  Per tile and
+// wave the matrix cores do 16 MFMAs of S^T = K Q^T and 16 of O^T += V^T P^T
+// (v_mfma_f32_32x32x16), 1024 cycles; the softmax is ~100 VALU operations.
+//
+// Step structure.  Step t of a wave issues the MFMAs of S(t+1) = K(t+1) Q^T
+// and O += V(t)^T P(t) back to back, then the vector work of tile t+1:
+// mask, column max, exponentials into the fp16 P^T operands, row sums, and
+// the in-place fp16 conversion of V(t+1); one barrier per step.  The two
+// waves of a SIMD drift apart within a step, so one's vector work fills the
+// other's matrix-core phase (measured: interleaving the two inside a wave
+// by hand was slower).
+//
+// Precision.  The probabilities enter P.V as fp16 (11-bit significand; one
+// bf16 rounding, 2^-9 relative, is 8x coarser and puts short-context rows
+// several 1e-3 off).  bf16 V is converted to fp16 in LDS (exact for every
+// bf16 value of magnitude in [2^-14, 65504]; smaller ones round to fp16
+// subnormals, larger ones overflow).  The softmax denominators are summed
+// (v_dot2_f32_f16, fp32 accumulate) from exactly the fp16 P that the P.V
+// product uses.
+//
+// Memory path (per tile, 4 chunks of 16 tokens; larger pages are read 16
+// rows at a time).  K and V both arrive by direct-to-LDS buffer loads, two
+// (D = 128) or one (D = 64) per wave and operand, issued NKS steps ahead
+// into rings of NKS (K) and NKS + 1 (V) tile slots: the kernel is bound by
+// the bytes each CU keeps in flight against the HBM latency under load.
+// Every load goes through a buffer resource that covers only the chunk's
+// live rows: rows past the context and chunks without an allocated page
+// read as zeros.
+//
+// LDS layouts (lane-contiguous for every read):
+//   K block (chunk pc, dims 32dq..+32), 1 KiB: DMA lane m holds
+//     K[16pc + m%16][32dq + 8(m/16) ..+8]; the S^T A operand (32 keys of
+//     block kb, dims 16cc..) of lane l sits in block (2kb + (l%32)/16, cc/2)
+//     at 16(l%16) + 256(l/32) + 512(cc%2).
+//   V region (kb, j2, md, half), 512 B (two of them, half 0 and 1, form the
+//   1 KiB block that one direct-to-LDS load fills): lane L's 8 bytes are
+//     V[32kb + 16j2 + 8half + 4(L/32) + (L%16)/4][32md + 16((L/16)%2) + 4(L%4) ..+4]
+//     (fp16), what one ds_read_b64_tr_b16 hands lane L as dim 32md + L%32
+//     of four keys; the keys follow the S^T accumulator's own order, so the
+//     P^T operand is a slice of the accumulator.
+#include "prefill_common.h"
+
+#include <type_traits>
+
+namespace dd_prefill {
+namespace {
+
+#ifndef DD_PF_NKS
+#define DD_PF_NKS 3
+#endif
+#ifndef DD_PF_RING
+#define DD_PF_RING 8
+#endif
+#ifndef DD_PF_TAB
+#define DD_PF_TAB 8192
+#endif
+constexpr int NKS = DD_PF_NKS;     // K tile slots: K(kt+NKS) and V(kt+NKS) are issued at step kt
+constexpr int NVS = NKS + 1;       // V tile slots: V(kt) is read while V(kt+1) is converted
+constexpr int kTabP = DD_PF_TAB;   // page-table entries staged in LDS per work item
+   // page-table entries staged in LDS per work item
+
+typedef __attribute__((address_space(3))) char lds_char;
+DD_DEV unsigned lds_addr(const void *p) { return (unsigned)(uintptr_t)(const lds_char *)p; }
+
+// LDS reads and writes in inline assembly: the compiler cannot relate them
+// to the direct-to-LDS loads in flight and would otherwise wait for all of
+// them.  A read's consumer waits with lgkm_wait(x, n), n = LDS operations
+// issued after it (they complete in order).
+DD_DEV u32x4 lds_read128(unsigned addr, int off) {
+  u32x4 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(off) : "memory");
+  return r;
+}
+DD_DEV u32x2 lds_read_tr(unsigned addr, int off) {
+  u32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(off) : "memory");
+  return r;
+}
+DD_DEV void lds_write128(unsigned addr, int off, u32x4 x) {
+  asm volatile("ds_write_b128 %0, %1 offset:%2" : : "v"(addr), "v"(x), "i"(off) : "memory");
+}
+// Every register an awaited read writes must be an operand of its wait:
+// otherwise the compiler may read that register before the wait.
+template <typename T>
+DD_DEV void lgkm_wait(T &x, int n) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(x) : "i"(n < 15 ? n : 15));
+}
+template <typename T>
+DD_DEV void lgkm_wait(T &x, T &y, int n) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(x), "+v"(y) : "i"(n < 15 ? n : 15));
+}
+DD_DEV void lgkm_drain() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+DD_DEV void barrier() { asm volatile("s_barrier" ::: "memory"); }
+// s_waitcnt vmcnt(n), no wait on the other counters
+template <int N>
+DD_DEV void vm_wait() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int DT>
+DD_DEV f32x16 mfma_s(u32x4 k, u32x4 q, f32x16 c) {
+  if constexpr (DT == DD_BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, k), __builtin_bit_cast(bf16x8, q), c,
+                                                   0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, k), __builtin_bit_cast(f16x8, q), c, 0,
+                                                  0, 0);
+  }
+}
+DD_DEV f32x16 mfma_o(u32x4 v, u32x4 p, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, v), __builtin_bit_cast(f16x8, p), c, 0, 0,
+                                                0);
+}
+
+DD_DEV unsigned cvt_pk_f16(float a, float b) {
+  return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{a, b}, f16x2));
+}
+// 8 bf16 -> 8 fp16 (exact in fp16's normal range)
+DD_DEV u32x4 bf16x8_to_f16x8(u32x4 x) {
+  u32x4 y;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) y[i] = cvt_pk_f16(__uint_as_float(x[i] << 16), __uint_as_float(x[i] & 0xffff0000u));
+  return y;
+}
+
+template <int DT, int D>
+__global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
+  static_assert(D == 64 || D == 128, "head sizes 64 and 128");
+  constexpr int NW = 8;
+  constexpr int NT = 64 * NW;
+  constexpr int KT = 64;                // keys per tile
+  constexpr int NCC = D / 16;           // k-steps of S^T
+  constexpr int MD = D / 32;            // 32-dim blocks of O^T
+  constexpr int DQ = D / 32;            // 1 KiB K blocks per 16-key chunk
+  constexpr int COLS = 32 * NW;
+  constexpr int PLANE = KT * D * 2;     // bytes of one K or V tile
+  constexpr int IPW = DQ / 2;           // K DMA instructions per wave per tile
+  constexpr int VJ = PLANE / (16 * NT); // 16-byte pieces per thread of a V tile
+  // loads issued after V(kt+2) that may still be in flight when this wave's
+  // K(kt+2) and V(kt+2) must have landed (end of step kt): the K/V loads of
+  // the NKS-2 later steps
+  constexpr int VMW = (NKS - 2) * 2 * IPW;
+  static_assert(NKS >= 3, "K/V tiles are issued at least three steps ahead");
+
+  __shared__ __align__(1024) char s_k[NKS * PLANE];
+  __shared__ __align__(1024) char s_v[NVS * PLANE];
+  __shared__ int s_tab[kTabP];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = uniform(tid >> 6);
+  const int l32 = lane & 31;
+  const int h2 = lane >> 5;
+
+  int grp, qt;
+  if (p.plan) {
+    const int item = p.plan[blockIdx.x];
+    if (item < 0) return;
+    grp = item / p.max_tiles;
+    qt = item - grp * p.max_tiles;
+  } else {
+    const int xcd = blockIdx.x & 7;
+    const int j = blockIdx.x >> 3;
+    grp = xcd + 8 * (j / p.max_tiles);
+    qt = p.max_tiles - 1 - j % p.max_tiles;
+  }
+  if (grp >= p.n * p.KH) return;
+  const int seg = grp / p.KH;
+  const int kh = grp - seg * p.KH;
+  const long tok0 = p.cu[seg];
+  const int len = (int)(p.cu[seg + 1] - tok0);
+  const int G = p.G;
+  const int rows = COLS / G;
+  const int r0 = qt * rows;
+  if (r0 >= len) return;
+  const int context = (int)p.ctx[seg];
+  const int start = context - len;
+  const long slot = p.slots[seg];
+  const int rows_here = min(rows, len - r0);
+
+  const int k_hi = start + r0 + rows_here;  // exclusive
+  const int k_lo = p.window > 0 ? max(0, start + r0 - p.window + 1) : 0;
+  const int kt_first = k_lo / KT;
+  const int kt_last = (k_hi - 1) / KT;
+
+  // page-table entries of the 16-key chunks this item visits
+  const int e_first = (kt_first * KT) >> p.page_shift;
+  const int e_count = (((kt_last + 1) * KT - 1) >> p.page_shift) - e_first + 1;
+  const bool slot_ok = slot >= 0 && slot < p.table_rows;
+  auto table_entry = [&](int e) {
+    const int phys = (slot_ok && e < p.table_w) ? p.table[slot * p.table_w + e] : -1;
+    return (phys >= 0 && phys < p.capacity) ? phys : -1;
+  };
+  for (int i = tid; i < e_count && i < kTabP; i += NT) s_tab[i] = table_entry(e_first + i);
+  auto table_at = [&](int e) -> int {   // wave-uniform
+    const int i = e - e_first;
+    return i < kTabP ? s_tab[i] : table_entry(e);
+  };
+
+  // ---- this lane's query column; Q^T operands (B of S^T) ----
+  const int col = w * 32 + l32;
+  const int qr = col / G;
+  const int gh = col - qr * G;
+  const bool colok = qr < rows_here;
+  const int qpos = start + r0 + (colok ? qr : 0);
+  u32x4 qb[NCC];
+  {
+    const long row = (tok0 + r0 + (colok ? qr : 0)) * p.H + (long)kh * G + gh;
+    const unsigned short *qsrc = (const unsigned short *)p.q + row * D + 8 * h2;
+#pragma unroll
+    for (int cc = 0; cc < NCC; ++cc) {
+      const u32x4 x = *(const u32x4 *)(qsrc + 16 * cc);   // row clamped into the segment
+      qb[cc] = colok ? x ^ p.q_sign : u32x4{0, 0, 0, 0};
+    }
+  }
+  __syncthreads();  // s_tab
+
+  // ---- loads ----
+  // K: wave w fills blocks w*IPW .. +IPW of a tile (chunk b / DQ, dims 32 (b % DQ)..)
+  const int kb0 = w * IPW;
+  const int k_chunk = kb0 / DQ;
+  const unsigned k_dma_lane = 2u * ((lane & 15) * D + 32 * (kb0 % DQ) + 8 * (lane >> 4));
+  // Page of one 16-key chunk of tile kt (-1: none, or past the last tile).
+  // The lookups for a step's loads are read from LDS during the previous
+  // step, so that no step starts by waiting for one.
+  auto lookup = [&](int kt, int chunk) __attribute__((always_inline)) -> int {
+    return kt <= kt_last ? table_at((kt * KT + 16 * chunk) >> p.page_shift) : -1;
+  };
+  // Buffer resource of the chunk's live rows; tiles past the last one load
+  // nothing (zero-size resource): loads are issued unconditionally so that
+  // every wait count is static.
+  auto chunk_rsrc = [&](const void *plane, int kt, int chunk, int phys_in) __attribute__((always_inline)) {
+    const int key0 = kt * KT + 16 * chunk;
+    const int phys = uniform(phys_in);
+    const int live = phys < 0 ? 0 : min(16, context - key0);
+    const long base =
+        phys < 0 ? 0 : ((((long)phys * p.KH + kh) << p.page_shift) | (key0 & (p.page - 1))) * (long)D;
+    return __builtin_amdgcn_make_buffer_rsrc((void *)uniform_ptr((const char *)plane + 2 * base), (short)0,
+                                             uniform(live > 0 ? live * D * 2 : 0), kBufferWord3);
+  };
+  auto issue_k = [&](int kt, int phys) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(p.k, kt, k_chunk, phys);
+    char *dst = s_k + ((kt - kt_first) % NKS) * PLANE + kb0 * 1024;
+#pragma unroll
+    for (int j = 0; j < IPW; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(dst + j * 1024), 16, k_dma_lane, 64 * j, 0, 0);
+  };
+  // V: blocks (chunk, md) of 1 KiB, the same chunk as K; DMA lane m of block
+  // (c, md) brings the 16 bytes V[16c + 8(m/32) + 4((m%32)/16) + ((m%32)/2)%4]
+  // [8q8 ..+8], q8 = 4md + 2(((m%32)/8)%2) + m%2: the two 8-byte pieces that
+  // the transposing read of region (c, md, half m/32) hands lanes 2(m%32)
+  // and 2(m%32)+1.  bf16 tiles are converted to fp16 in place afterwards.
+  const int vb0 = w * IPW;
+  const unsigned v_dma_lane = [&] {
+    const int m = lane & 31;
+    const int key = 8 * (lane >> 5) + 4 * (m >> 4) + ((m >> 1) & 3);
+    const int q8 = 4 * (vb0 % MD) + 2 * ((m >> 3) & 1) + (m & 1);
+    return (unsigned)(key * D * 2 + 16 * q8);
+  }();
+  auto issue_v = [&](int kt, int phys) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(p.v, kt, k_chunk, phys);
+    char *dst = s_v + ((kt - kt_first) % NVS) * PLANE + vb0 * 1024;
+#pragma unroll
+    for (int j = 0; j < IPW; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(dst + j * 1024), 16, v_dma_lane, 64 * j, 0, 0);
+  };
+  const unsigned v_base = lds_addr(s_v);
+  // bf16 V tile kt -> fp16 in place (16 contiguous bytes per lane)
+  auto convert_v = [&](int kt) __attribute__((always_inline)) {
+    if constexpr (DT == DD_BF16) {
+      const unsigned base = v_base + ((kt - kt_first) % NVS) * PLANE + 16u * tid;
+      u32x4 x[VJ];
+#pragma unroll
+      for (int j = 0; j < VJ; ++j) x[j] = lds_read128(base, j * 16 * NT);
+#pragma unroll
+      for (int j = 0; j < VJ; ++j) lgkm_wait(x[j], 0);
+#pragma unroll
+      for (int j = 0; j < VJ; ++j) lds_write128(base, j * 16 * NT, bf16x8_to_f16x8(x[j]));
+    }
+  };
+
+  // ---- S^T of one tile: two 32-key blocks ----
+  const unsigned k_rd = lds_addr(s_k) + 1024u * DQ * ((lane >> 4) & 1) + 16u * (lane & 15) + 256u * h2;
+  auto compute_s = [&](int kt, f32x16 (&s)[2]) __attribute__((always_inline)) {
+    const unsigned kb_addr = k_rd + (unsigned)(((kt - kt_first) % NKS) * PLANE);
+    // operand i = (cc, b) = (i / 2, i % 2); R reads in flight
+    constexpr int N = 2 * NCC, R = 4;
+    auto rd = [&](int i) __attribute__((always_inline)) {
+      const int cc = i >> 1, b = i & 1;
+      return lds_read128(kb_addr, (2 * b * DQ + cc / 2) * 1024 + 512 * (cc & 1));
+    };
+    u32x4 kop[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) kop[i] = rd(i);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int cc = i >> 1, b = i & 1;
+      lgkm_wait(kop[i % R], min(R - 1, N - 1 - i));
+      s[b] = mfma_s<DT>(kop[i % R], qb[cc], cc == 0 ? f32x16{} : s[b]);
+      if (i + R < N) kop[i % R] = rd(i + R);
+    }
+  };
+  f32x16 o[MD];
+#pragma unroll
+  for (int md = 0; md < MD; ++md) o[md] = f32x16{};
+  float m_run = kNegInf;
+  float l_part = 0.f;   // this lane's share of the column's denominator
+
+  const float sc = p.scale_log2;
+  const float slack = kMaxSlack / sc;
+  const unsigned v_rd = v_base + 8u * lane;
+
+  // ---- softmax pieces ----
+  // Bookkeeping of tile kt from its column max: the exponent offset mu; O
+  // and l are rescaled when the running max moves.
+  auto softmax_begin = [&](float mx) __attribute__((always_inline)) -> float {
+    const bool up = mx > m_run + slack;   // m_run = -inf moves to any finite max
+    const float mn = up ? mx : m_run;
+    const float mu = mn == kNegInf ? 0.f : mn * sc;
+    const float alpha = up ? __builtin_amdgcn_exp2f(m_run * sc - mu) : 1.f;
+    m_run = mn;
+    if (__builtin_amdgcn_ballot_w64(up)) {
+#pragma unroll
+      for (int md = 0; md < MD; ++md) o[md] *= alpha;
+      l_part *= alpha;
+    }
+    return mu;
+  };
+  // Probabilities 2i, 2i+1 of this lane (i < 16: block i / 8, registers
+  // 2 (i % 8) ..+2) into the fp16 P^T operands, and into the row sum.
+  auto softmax_pair = [&](f32x16 (&s)[2], int i, float mu, u32x4 (&pp)[2][2], float &lsum)
+      __attribute__((always_inline)) {
+    const int b = i >> 3, r = 2 * (i & 7);
+    const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[b][r], sc, -mu));
+    const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[b][r + 1], sc, -mu));
+    const unsigned h = cvt_pk_f16(e0, e1);
+    pp[b][(i & 7) >> 2][i & 3] = h;
+    lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, h), f16x2{(_Float16)1.f, (_Float16)1.f}, lsum, false);
+  };
+  // mask of tile kt (keys past a column's diagonal or before its window);
+  // key of register r of block b is kt*64 + 32b + 8(r/4) + 4h2 + r%4
+  auto mask = [&](int kt, f32x16 (&s)[2]) __attribute__((always_inline)) {
+    const int kbase = kt * KT;
+    if (!(kbase + KT - 1 <= start + r0 && (p.window == 0 || kbase >= start + r0 + rows_here - p.window))) {
+      const int lo = p.window > 0 ? qpos - p.window + 1 : -1;
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kbase + 32 * b + 8 * (r >> 2) + 4 * h2 + (r & 3);
+          s[b][r] = ((key <= qpos) & (key >= lo)) ? s[b][r] : kNegInf;
+        }
+      }
+    }
+  };
+  // partial column max over registers 4i .. 4i+3 of both blocks
+  auto max_part = [&](f32x16 (&s)[2], int i, float &mx) __attribute__((always_inline)) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) mx = fmaxf(fmaxf(mx, s[b][4 * i]), s[b][4 * i + 1]);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) mx = fmaxf(fmaxf(mx, s[b][4 * i + 2]), s[b][4 * i + 3]);
+  };
+
+  // ---- matrix-core phase of step kt: S(kt+1) = K(kt+1) Q^T (when there is
+  // a tile kt+1), then O += V(kt)^T P(kt).  One stream of LDS operands: K
+  // operands (one ds_read_b128 each), then V^T operands (two transposing
+  // reads each), R operands in flight.  The step's loads are issued after
+  // the first MFMAs, so that any wait for the memory pipeline overlaps them.
+  auto mfma_phase = [&](auto has_next_c, int kt, f32x16 (&s)[2], const u32x4 (&pp)[2][2], auto &&loads)
+      __attribute__((always_inline)) {
+    constexpr bool HN = decltype(has_next_c)::value;
+    constexpr int NS = HN ? 2 * NCC : 0, NV = 4 * MD, N = NS + NV, R = DD_PF_RING;
+    const unsigned kb_addr = k_rd + (unsigned)(((kt + 1 - kt_first) % NKS) * PLANE);
+    const unsigned vb = v_rd + (unsigned)(((kt - kt_first) % NVS) * PLANE);
+    // operand i < NS: one K read; else two transposing reads
+    u32x4 kop[R];
+    u32x2 lo[R], hi[R];
+    auto rd = [&](int i) __attribute__((always_inline)) {
+      if (i < NS) {
+        const int cc = i >> 1, b = i & 1;
+        kop[i % R] = lds_read128(kb_addr, (2 * b * DQ + cc / 2) * 1024 + 512 * (cc & 1));
+      } else {
+        const int j = i - NS;
+        lo[i % R] = lds_read_tr(vb, 2 * j * 512);
+        hi[i % R] = lds_read_tr(vb, 2 * j * 512 + 512);
+      }
+    };
+    // LDS instructions issued after operand i while it is awaited
+    auto after = [](int i) constexpr {
+      int n = 0;
+      for (int j = i + 1; j < i + R && j < N; ++j) n += j < NS ? 1 : 2;
+      return n;
+    };
+#pragma unroll
+    for (int i = 0; i < R; ++i) rd(i);
+    if constexpr (!HN) loads();
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      if (i < NS) {
+        const int cc = i >> 1, b = i & 1;
+        lgkm_wait(kop[i % R], after(i));
+        s[b] = mfma_s<DT>(kop[i % R], qb[cc], cc == 0 ? f32x16{} : s[b]);
+      } else {
+        const int j = i - NS, md = j % MD, bj = j / MD;
+        lgkm_wait(lo[i % R], hi[i % R], after(i));
+        const u32x4 op = {lo[i % R][0], lo[i % R][1], hi[i % R][0], hi[i % R][1]};
+        o[md] = mfma_o(op, pp[bj >> 1][bj & 1], o[md]);
+      }
+      if (i + R < N) rd(i + R);
+      if (HN && i == 1) loads();
+    }
+  };
+
+  // ---- vector phase of step kt: P(kt+1) from S(kt+1); V(kt+1) to fp16 in
+  // its LDS slot; the page numbers of the next step's loads ----
+  auto valu_phase = [&](int kt, f32x16 (&s)[2], u32x4 (&pp)[2][2])
+      __attribute__((always_inline)) {
+    mask(kt + 1, s);
+    float m = kNegInf;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) max_part(s, i, m);
+    const float mu = softmax_begin(xor32_max(m));
+    float lsum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) softmax_pair(s, i, mu, pp, lsum);
+    l_part += lsum;
+    // V(kt+1) of every wave landed before the previous barrier; this wave's
+    // K(kt+2) and V(kt+2) land before the next one
+    convert_v(kt + 1);
+    vm_wait<VMW>();
+  };
+
+  // ---- prologue: K and V of tiles f .. f+NKS-1 in flight, V(f) in fp16, P(f) ----
+  f32x16 s[2];
+  u32x4 pp[2][2];   // P(kt) as fp16 P^T operands
+#pragma unroll
+  for (int i = 0; i < NKS; ++i) {
+    const int ph = lookup(kt_first + i, k_chunk);
+    issue_k(kt_first + i, ph);
+    issue_v(kt_first + i, ph);
+  }
+  int pk = lookup(kt_first + NKS, k_chunk);
+  vm_wait<VMW>();   // K and V of tiles f and f+1 have landed
+  barrier();        // ... for every wave
+  convert_v(kt_first);
+  lgkm_drain();
+  barrier();
+  compute_s(kt_first, s);
+  {
+    mask(kt_first, s);
+    float m = kNegInf;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) max_part(s, i, m);
+    const float mu = softmax_begin(xor32_max(m));
+    float lsum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) softmax_pair(s, i, mu, pp, lsum);
+    l_part += lsum;
+  }
+  barrier();   // every wave has read K(kt_first) before step kt_first reloads its slot
+
+  // ---- steady state ----
+  // Step kt: K(kt+NKS) into the slot of K(kt) and V(kt+NKS) into the slot of
+  // V(kt-1) (zero-size past the last tile, so that every wait count is
+  // static); S(kt+1) and O += V(kt) P(kt) on the matrix cores; P(kt+1) and
+  // V(kt+1) to fp16 on the vector ALU; barrier.
+  for (int kt = kt_first; kt <= kt_last; ++kt) {
+    // this step's page number, read from LDS during the previous step, into
+    // a scalar register now (no LDS operation of this wave is in flight)
+    int pku = uniform(pk);
+    asm volatile("" : "+s"(pku));
+    auto loads = [&]() __attribute__((always_inline)) {
+      issue_k(kt + NKS, pku);
+      issue_v(kt + NKS, pku);
+    };
+    if (kt + 1 <= kt_last) {
+      mfma_phase(std::true_type{}, kt, s, pp, loads);
+      valu_phase(kt, s, pp);
+      pk = lookup(kt + NKS + 1, k_chunk);
+      lgkm_drain();
+      barrier();
+    } else {
+      mfma_phase(std::false_type{}, kt, s, pp, loads);
+    }
+  }
+  vm_wait<0>();   // no load outlives the workgroup
+
+  // ---- normalise and store: lane holds dims 32md + 8(r/4) + 4h2 + r%4 of its column ----
+  const float l = xor32_sum(l_part);
+  if (!colok) return;
+  const float inv = 1.f / l;
+  const long orow = ((tok0 + r0 + qr) * p.H + (long)kh * G + gh) * D;
+  unsigned short *dst = (unsigned short *)p.out;
+#pragma unroll
+  for (int md = 0; md < MD; ++md) {
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const f32x16 &x = o[md];
+      const u32x2 pk = {pack2<DT>(x[4 * q4 + 0] * inv, x[4 * q4 + 1] * inv),
+                        pack2<DT>(x[4 * q4 + 2] * inv, x[4 * q4 + 3] * inv)};
+      *(u32x2 *)(dst + orow + 32 * md + 8 * q4 + 4 * h2) = pk;
+    }
+  }
+}
+
+template <int DT, int D>
+int launch_pipe(PrefillParams p, int max_len, int plan_len, hipStream_t s) {
+  constexpr int COLS = 256;
+  if (COLS / p.G < 1) return DD_EUNSUPPORTED;
+  p.max_tiles = (int)dd_cdiv(max_len, COLS / p.G);
+  const long grid = p.plan ? (long)plan_len : 8L * dd_cdiv((long)p.n * p.KH, 8) * p.max_tiles;
+  if (grid == 0) return DD_OK;
+  if (grid > 0x7fffffffL) return DD_EUNSUPPORTED;
+  hipLaunchKernelGGL((prefill_pipe_kernel<DT, D>), dim3((unsigned)grid), dim3(512), 0, s, p);
+  DD_LAUNCH_CHECK();
+  return DD_OK;
+}
+
+}  // namespace
+
+int prefill_pipe_dispatch(const PrefillParams &p, int dtype, int dim, int max_len, int plan_len, hipStream_t s) {
+  if (dtype == DD_BF16) {
+    if (dim == 64) return launch_pipe<DD_BF16, 64>(p, max_len, plan_len, s);
+    if (dim == 128) return launch_pipe<DD_BF16, 128>(p, max_len, plan_len, s);
+  } else if (dtype == DD_F16) {
+    if (dim == 64) return launch_pipe<DD_F16, 64>(p, max_len, plan_len, s);
+    if (dim == 128) return launch_pipe<DD_F16, 128>(p, max_len, plan_len, s);
+  }
+  return DD_EUNSUPPORTED;
+}
+
+}  // namespace dd_prefill
