@@ -199,7 +199,6 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
     const int phys = (slot_ok && e < p.table_w) ? p.table[slot * p.table_w + e] : -1;
     return (phys >= 0 && phys < p.capacity) ? phys : -1;
   };
-  for (int i = tid; i < e_count && i < kTabP; i += NT) s_tab[i] = table_entry(e_first + i);
   auto table_at = [&](int e) -> int {   // wave-uniform
     const int i = e - e_first;
     return i < kTabP ? s_tab[i] : table_entry(e);
@@ -211,17 +210,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   const int gh = col - qr * G;
   const bool colok = qr < rows_here;
   const int qpos = start + r0 + (colok ? qr : 0);
-  u32x4 qb[NCC];
-  {
-    const long row = (tok0 + r0 + (colok ? qr : 0)) * p.H + (long)kh * G + gh;
-    const unsigned short *qsrc = (const unsigned short *)p.q + row * D + 8 * h2;
-#pragma unroll
-    for (int cc = 0; cc < NCC; ++cc) {
-      const u32x4 x = *(const u32x4 *)(qsrc + 16 * cc);   // row clamped into the segment
-      qb[cc] = colok ? x ^ p.q_sign : u32x4{0, 0, 0, 0};
-    }
-  }
-  __syncthreads();  // s_tab
+  u32x4 qb[NCC];   // loaded in the prologue
 
   // ---- loads ----
   // K: wave w fills blocks w*IPW .. +IPW of a tile (chunk b / DQ, dims 32 (b % DQ)..)
@@ -441,12 +430,26 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   // ---- prologue: K and V of tiles f .. f+NKS-1 in flight, V(f) in fp16, P(f) ----
   f32x16 s[2];
   u32x4 pp[2][2];   // P(kt) as fp16 P^T operands
+  // The first tiles' pages come straight from the page table, so that their
+  // loads are in flight while Q and the LDS copy of the table are fetched.
 #pragma unroll
   for (int i = 0; i < NKS; ++i) {
-    const int ph = lookup(kt_first + i, k_chunk);
-    issue_k(kt_first + i, ph);
-    issue_v(kt_first + i, ph);
+    const int kt = kt_first + i;
+    const int ph = kt <= kt_last ? table_entry((kt * KT + 16 * k_chunk) >> p.page_shift) : -1;
+    issue_k(kt, ph);
+    issue_v(kt, ph);
   }
+  {
+    const long row = (tok0 + r0 + (colok ? qr : 0)) * p.H + (long)kh * G + gh;
+    const unsigned short *qsrc = (const unsigned short *)p.q + row * D + 8 * h2;
+#pragma unroll
+    for (int cc = 0; cc < NCC; ++cc) {
+      const u32x4 x = *(const u32x4 *)(qsrc + 16 * cc);   // row clamped into the segment
+      qb[cc] = colok ? x ^ p.q_sign : u32x4{0, 0, 0, 0};
+    }
+  }
+  for (int i = tid; i < e_count && i < kTabP; i += NT) s_tab[i] = table_entry(e_first + i);
+  __syncthreads();  // s_tab
   int pk = lookup(kt_first + NKS, k_chunk);
   vm_wait<VMW>();   // K and V of tiles f and f+1 have landed
   barrier();        // ... for every wave
@@ -472,25 +475,23 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   // V(kt-1) (zero-size past the last tile, so that every wait count is
   // static); S(kt+1) and O += V(kt) P(kt) on the matrix cores; P(kt+1) and
   // V(kt+1) to fp16 on the vector ALU; barrier.
-  for (int kt = kt_first; kt <= kt_last; ++kt) {
+  // (the last step, which has no tile kt+1, is peeled off so that the loop
+  // body has one path and the O accumulators keep their registers)
+  for (int kt = kt_first; kt < kt_last; ++kt) {
     // this step's page number, read from LDS during the previous step, into
     // a scalar register now (no LDS operation of this wave is in flight)
     int pku = uniform(pk);
     asm volatile("" : "+s"(pku));
-    auto loads = [&]() __attribute__((always_inline)) {
+    mfma_phase(std::true_type{}, kt, s, pp, [&]() __attribute__((always_inline)) {
       issue_k(kt + NKS, pku);
       issue_v(kt + NKS, pku);
-    };
-    if (kt + 1 <= kt_last) {
-      mfma_phase(std::true_type{}, kt, s, pp, loads);
-      valu_phase(kt, s, pp);
-      pk = lookup(kt + NKS + 1, k_chunk);
-      lgkm_drain();
-      barrier();
-    } else {
-      mfma_phase(std::false_type{}, kt, s, pp, loads);
-    }
+    });
+    valu_phase(kt, s, pp);
+    pk = lookup(kt + NKS + 1, k_chunk);
+    lgkm_drain();
+    barrier();
   }
+  mfma_phase(std::false_type{}, kt_last, s, pp, [] {});
   vm_wait<0>();   // no load outlives the workgroup
 
   // ---- normalise and store: lane holds dims 32md + 8(r/4) + 4h2 + r%4 of its column ----
