@@ -23,8 +23,11 @@ FLAGS = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}',
          '-Wno-unused-command-line-argument']
 
 
-# Per-source extra flags (none at present).
-SOURCE_FLAGS = {}
+# Per-source extra flags.  The streamed decode kernels keep their MFMA
+# accumulators in VGPRs: in the AGPR form the compiler copies them between
+# the two register files on every loop iteration.
+_VGPR_MFMA = ['-mllvm', '-amdgpu-mfma-vgpr-form=1']
+SOURCE_FLAGS = {'decode_bf16.hip': _VGPR_MFMA, 'decode_f16.hip': _VGPR_MFMA, 'decode_i8.hip': _VGPR_MFMA}
 
 
 def _compile(source, obj, extra=()):

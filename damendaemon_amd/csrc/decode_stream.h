@@ -33,6 +33,7 @@
 // and of V^T (4 rows x 32 bytes per 16 lanes) hit distinct LDS banks.
 #pragma once
 #include <type_traits>
+#include <utility>
 
 namespace dd_decode {
 
@@ -52,6 +53,18 @@ typedef __attribute__((address_space(3))) void lds_void;
 #ifndef DD_STREAM_NW64
 #define DD_STREAM_NW64 4
 #endif
+
+// f(integral_constant<int, I>) for I = 0 .. N-1, unrolled at compile time.
+template <typename F, int... I>
+DD_DEV void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+DD_DEV void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+
 #ifndef DD_STREAM_NW128
 #define DD_STREAM_NW128 4
 #endif
@@ -300,10 +313,13 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
   const char *kplane = (const char *)p.k;
   const char *vplane = (const char *)p.v;
   const __attribute__((address_space(4))) int32_t *tab = (const __attribute__((address_space(4))) int32_t *)p.table;
-  // Chunk i of this wave into `stage`.  Chunks past the wave's last one are
-  // issued too, with an empty resource (no memory traffic): every iteration
-  // then has the same loads in flight and waits for a constant count.
-  auto issue = [&](int i, int stage) __attribute__((always_inline)) {
+  // Buffer resources of chunk i of this wave (K, V).  Chunks past the wave's
+  // last one get an empty resource (no memory traffic): every iteration then
+  // has the same loads in flight and waits for a constant count.
+  struct ChunkRsrc {
+    __amdgpu_buffer_rsrc_t k, v;
+  };
+  auto chunk_rsrc = [&](int i) __attribute__((always_inline)) -> ChunkRsrc {
     const int pg = first + i * NW;
     long base;  // element offset of the chunk's first row, -1 when unmapped
     if (i >= n) {
@@ -323,18 +339,21 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
     const int live = base < 0 ? 0 : max(0, min(16, s_hi - pg * 16));
     const long off = base < 0 ? 0 : 2 * base;
     const int bytes = uniform(live * ROWB);
-    const __amdgpu_buffer_rsrc_t rk =
-        __builtin_amdgcn_make_buffer_rsrc((void *)uniform_ptr(kplane + off), (short)0, bytes, kRawBufferWord3);
-    const __amdgpu_buffer_rsrc_t rv =
-        __builtin_amdgcn_make_buffer_rsrc((void *)uniform_ptr(vplane + off), (short)0, bytes, kRawBufferWord3);
+    return ChunkRsrc{
+        __builtin_amdgcn_make_buffer_rsrc((void *)uniform_ptr(kplane + off), (short)0, bytes, kRawBufferWord3),
+        __builtin_amdgcn_make_buffer_rsrc((void *)uniform_ptr(vplane + off), (short)0, bytes, kRawBufferWord3)};
+  };
+  // Chunk i straight into LDS `stage` (direct-to-LDS loads).
+  auto issue = [&](int i, int stage) __attribute__((always_inline)) {
+    const ChunkRsrc r = chunk_rsrc(i);
     char *dst = s_ring + (w * NB + stage) * STAGE;
 #pragma unroll
     for (int j = 0; j < IPP; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void *)(dst + 1024 * j), 16, dma_off[j], 0, 0,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r.k, (lds_void *)(dst + 1024 * j), 16, dma_off[j], 0, 0,
                                                kStreamLoadAux);
 #pragma unroll
     for (int j = 0; j < IPP; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void *)(dst + PAGEB + 1024 * j), 16, dma_off[j], 0, 0,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r.v, (lds_void *)(dst + PAGEB + 1024 * j), 16, dma_off[j], 0, 0,
                                                kStreamLoadAux);
   };
 
@@ -444,22 +463,20 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
 #pragma unroll
   for (int c = 0; c < NC; ++c) after_wait(qa[c]);
   after_wait(slope);
-  // Chunk i: NB - 1 younger chunks (2 IPP loads each) stay in flight.
-  for (int i0 = 0; i0 < n; i0 += NB) {
-#define DD_STREAM_STEP(U)                                                  \
-    if constexpr (U < NB) {                                                \
-      const int i = i0 + U;                                                \
-      if (i < n) {                                                         \
-        wait_vm<2 * IPP * (NB - 1)>();                                     \
-        consume(i, std::integral_constant<int, (U < NB ? U : 0)>{});       \
-      }                                                                    \
-    }
-    DD_STREAM_STEP(0)
-    DD_STREAM_STEP(1)
-    DD_STREAM_STEP(2)
-    DD_STREAM_STEP(3)
-#undef DD_STREAM_STEP
-  }
+  // Chunk i: NB - 1 younger chunks (2 IPP loads each) stay in flight.  Full
+  // groups of NB chunks run without guards and the last n % NB after the
+  // loop, so that the loop body has one path and the accumulators keep
+  // their registers across iterations.
+  auto step = [&](int i, auto u_tag) __attribute__((always_inline)) {
+    wait_vm<2 * IPP * (NB - 1)>();
+    consume(i, u_tag);
+  };
+  int i0 = 0;
+  for (; i0 + NB <= n; i0 += NB)
+    static_for<NB>([&](auto u) __attribute__((always_inline)) { step(i0 + decltype(u)::value, u); });
+  static_for<NB - 1>([&](auto u) __attribute__((always_inline)) {
+    if (i0 + decltype(u)::value < n) step(i0 + decltype(u)::value, u);
+  });
   wait_vm<0>();  // the trailing (empty) loads, before the ring is reused
 
   stream_epilogue<DT, D, NW>(p, s_ml, (float *)s_ring, o, m_run, lsum, w, lane, b, kh, split);
@@ -510,6 +527,29 @@ DD_DEV constexpr int i8_swz(int R) {
   } else {
     return ((R & 1) | (((R >> 1) & 1) << 1) | (((R >> 2) & 1) << 2) | (hi << 3)) << 1;
   }
+}
+
+// int8 -> fp16 for the matrix cores: byte b (two's complement) becomes the
+// fp16 number 1152 + b, exactly: b ^ 0x80 = b + 128 in [0, 255] is the low
+// mantissa byte of an fp16 whose high byte is 0x64 (1024 + mantissa).  One
+// XOR per 4 bytes and one byte permute per 2.
+constexpr float kI8Offset = 1152.f;
+DD_DEV u32x4 widen_i8x8_off(u32x2 w) {
+  const unsigned a = w[0] ^ 0x80808080u, b = w[1] ^ 0x80808080u;
+  constexpr unsigned kHi = 0x64646464u;
+  // v_perm_b32(src0, src1, sel): bytes 0-3 of src1, 4-7 of src0
+  return u32x4{__builtin_amdgcn_perm(a, kHi, 0x00050004u), __builtin_amdgcn_perm(a, kHi, 0x00070006u),
+               __builtin_amdgcn_perm(b, kHi, 0x00050004u), __builtin_amdgcn_perm(b, kHi, 0x00070006u)};
+}
+DD_DEV unsigned cvt_pk_f16(float a, float b) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
+}
+// acc + lo(a) * lo(b) + hi(a) * hi(b) on fp16 pairs, fp32 accumulate
+DD_DEV float dot2_f16(unsigned a, unsigned b, float acc) {
+  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), acc, false);
 }
 
 template <int QT, int D, int NG, int NB, int NW>
@@ -662,11 +702,36 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
     }
   };
 
+  // Everything enters the matrix cores as fp16 (see the int8 section note):
+  // K and V bytes as exact fp16 values b + 1152, Q converted to fp16, the
+  // probabilities p * v_scale as fp16.  The 1152 offsets come out of S^T
+  // through the column sums of Q (qoff) and out of O^T through the column
+  // sums of the fp16 P^T operands (psum).
+  u32x4 qh[NC];
+  float qoff[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    after_wait(qa[c]);
+    if constexpr (QT == DD_BF16) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qh[c][j] = cvt_pk_f16(bf16_lo(qa[c][j]), bf16_hi(qa[c][j]));
+    } else {
+      qh[c] = qa[c];
+    }
+    float qs = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qs = dot2_f16(qh[c][j], 0x3C003C00u, qs);
+    qoff[c] = kI8Offset * xor32_sum(xor16_sum(qs));   // column n16's sum over the 32 dims of chunk c
+  }
+
   f32x4 o[MD];
 #pragma unroll
   for (int md = 0; md < MD; ++md) o[md] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = kNegInf;
-  float lsum = 0.f;
+  float m_run = kNegInf;   // running max of logit + exponent of the V scale
+  float lsum = 0.f;        // sum of exp2(logit - m_run)
+  float psum[NG];          // sums of the fp16 P^T operands (this lane's keys)
+#pragma unroll
+  for (int g = 0; g < NG; ++g) psum[g] = 0.f;
 
   auto consume = [&](int i, auto stage_tag) __attribute__((always_inline)) {
     constexpr int SO = decltype(stage_tag)::value * STAGE;
@@ -708,28 +773,38 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
       const unsigned wd = sc[ch][idx >> 2][(idx >> 1) & 1];
       return half_bits_to_float((unsigned short)((idx & 1) ? (wd >> 16) : (wd & 0xffffu)));
     };
-
-    // logits: s[ch][e] = key t0 + 16 ch + 4 kg + e for head n16
-    float x[2][4];
+    // The common case -- every key of the pair inside [s_lo, s_hi), no ALiBi,
+    // no relative bias -- runs a copy of the step without masks or bias terms.
+    auto body = [&](auto fast_tag) __attribute__((always_inline)) {
+    constexpr bool FAST = decltype(fast_tag)::value;
+    // logits x = key t0 + 16 ch + 4 kg + e for head n16; y adds the exponent
+    // of the key's largest V scale (the quantity the running max tracks)
+    float x[2][4], y[2][4], vsf[2][4][NG];
     float mx = kNegInf;
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
       f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
       if constexpr (NG == 1) {
+        float qo = 0.f;
 #pragma unroll
-        for (int c = 0; c < NC; ++c) sacc = mfma16x16x32<QT>(widen_i8x8<QT>(k8[ch][c]), qa[c], sacc);
+        for (int c = 0; c < NC; ++c) {
+          sacc = mfma16x16x32<DD_F16>(widen_i8x8_off(k8[ch][c]), qh[c], sacc);
+          qo += qoff[c];
+        }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sacc[e] *= scale_of(ks8, ch, e, 0);
+        for (int e = 0; e < 4; ++e) sacc[e] = (sacc[e] - qo) * (scale_of(ks8, ch, e, 0) * p.scale_log2);
       } else {
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-          const f32x4 part = mfma16x16x32<QT>(widen_i8x8<QT>(k8[ch][c]), qa[c], f32x4{0.f, 0.f, 0.f, 0.f});
+          const f32x4 part = mfma16x16x32<DD_F16>(widen_i8x8_off(k8[ch][c]), qh[c], f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-          for (int e = 0; e < 4; ++e) sacc[e] += scale_of(ks8, ch, e, c) * part[e];
+          for (int e = 0; e < 4; ++e) sacc[e] += scale_of(ks8, ch, e, c) * (part[e] - qoff[c]);
         }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sacc[e] *= p.scale_log2;
       }
       float rb[4] = {0.f, 0.f, 0.f, 0.f};
-      if (p.rel) {  // workgroup-uniform
+      if (!FAST && p.rel) {  // workgroup-uniform
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int t = t0 + 16 * ch + 4 * kg + e;
@@ -741,9 +816,19 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int t = t0 + 16 * ch + 4 * kg + e;
-        const float v = sacc[e] * p.scale_log2 + slope * (float)t + rb[e];
-        x[ch][e] = (t >= s_lo && t < s_hi) ? v : kNegInf;
-        mx = fmaxf(mx, x[ch][e]);
+        const bool live = FAST || (t >= s_lo && t < s_hi);
+        const float v = FAST ? sacc[e] : sacc[e] + slope * (float)t + rb[e];
+        int ex = 0;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          // dead keys' scales may be garbage: they enter P as 0
+          vsf[ch][e][g] = live ? scale_of(vs8, ch, e, g) : 0.f;
+          ex = g == 0 ? __builtin_amdgcn_frexp_expf(vsf[ch][e][g])
+                      : max(ex, __builtin_amdgcn_frexp_expf(vsf[ch][e][g]));
+        }
+        x[ch][e] = live ? v : kNegInf;
+        y[ch][e] = live ? v + (float)ex : kNegInf;
+        mx = fmaxf(mx, y[ch][e]);
       }
     }
     mx = xor32_max(xor16_max(mx));
@@ -754,9 +839,13 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
       m_run = mn;
       lsum *= alpha;
 #pragma unroll
+      for (int g = 0; g < NG; ++g) psum[g] *= alpha;
+#pragma unroll
       for (int md = 0; md < MD; ++md) o[md] *= alpha;
     }
     const float mu = m_run == kNegInf ? 0.f : m_run;
+    // p = exp2(x - mu) <= 2^(8 - exponent of the key's V scale), so every
+    // p * v_scale <= 2^8 fits fp16; dead keys have p = 0.
     float pr[2][4];
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch)
@@ -766,78 +855,53 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
         lsum += pr[ch][e];
       }
     // P^T operand per V scale group: slot j < 4 is key 4kg + j of chunk 0,
-    // slot j >= 4 key 4kg + j - 4 of chunk 1.  Dead keys have p = 0 and
-    // their (possibly garbage) scales are dropped.  p * scale is split into
-    // a high and a low 16-bit part (two MFMAs), so the fp16 scale keeps its
-    // full precision: with a single key the output is exactly int8 * scale.
-    u32x4 pb[NG], pl[NG];
+    // slot j >= 4 key 4kg + j - 4 of chunk 1.
+    u32x4 pb[NG];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      float q[8], r[8];
 #pragma unroll
-      for (int ch = 0; ch < 2; ++ch)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int t = t0 + 16 * ch + 4 * kg + e;
-          const float sc = (t >= s_lo && t < s_hi) ? scale_of(vs8, ch, e, g) : 0.f;
-          q[4 * ch + e] = pr[ch][e] * sc;
-        }
-      pb[g] = u32x4{pack_pair<QT>(q[0], q[1]), pack_pair<QT>(q[2], q[3]), pack_pair<QT>(q[4], q[5]),
-                    pack_pair<QT>(q[6], q[7])};
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const unsigned wd = pb[g][j >> 1];
-        const unsigned short hb = (unsigned short)((j & 1) ? (wd >> 16) : (wd & 0xffffu));
-        const float hi = QT == DD_BF16 ? __uint_as_float((unsigned)hb << 16) : half_bits_to_float(hb);
-        r[j] = q[j] - hi;
+      for (int j = 0; j < 4; ++j) {
+        const int ch = j >> 1, e = 2 * (j & 1);
+        pb[g][j] = cvt_pk_f16(pr[ch][e] * vsf[ch][e][g], pr[ch][e + 1] * vsf[ch][e + 1][g]);
+        psum[g] = dot2_f16(pb[g][j], 0x3C003C00u, psum[g]);
       }
-      pl[g] = u32x4{pack_pair<QT>(r[0], r[1]), pack_pair<QT>(r[2], r[3]), pack_pair<QT>(r[4], r[5]),
-                    pack_pair<QT>(r[6], r[7])};
-    }
-    // Keys before the window start hold expired (possibly NaN) rows: zero
-    // their bytes in the V^T operand.  Byte j of a lane is key slot j.
-    if (t0 < s_lo) {
-      unsigned mlo = 0, mhi = 0;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int t = t0 + 16 * (j >> 2) + 4 * kg + (j & 3);
-        if (t >= s_lo) {
-          if (j < 4) mlo |= 0xffu << (8 * j);
-          else mhi |= 0xffu << (8 * (j - 4));
-        }
-      }
-#pragma unroll
-      for (int md = 0; md < MD; ++md) v8[md] = u32x2{v8[md][0] & mlo, v8[md][1] & mhi};
     }
 #pragma unroll
     for (int md = 0; md < MD; ++md) {
       const int g = NG == 1 ? 0 : (16 * md) / 32;
-      const u32x4 vw = widen_i8x8<QT>(v8[md]);
-      o[md] = mfma16x16x32<QT>(vw, pl[g], mfma16x16x32<QT>(vw, pb[g], o[md]));
+      o[md] = mfma16x16x32<DD_F16>(widen_i8x8_off(v8[md]), pb[g], o[md]);
+    }
+    };
+    if (t0 >= s_lo && t0 + 32 <= s_hi && !p.alibi && !p.rel) {
+      body(std::true_type{});
+    } else {
+      body(std::false_type{});
     }
   };
 
 #pragma unroll
   for (int u = 0; u < NB; ++u) issue(u, u);
-#pragma unroll
-  for (int c = 0; c < NC; ++c) after_wait(qa[c]);
   after_wait(slope);
-  for (int i0 = 0; i0 < n; i0 += NB) {
-#define DD_STREAM_STEP(U)                                                  \
-    if constexpr (U < NB) {                                                \
-      const int i = i0 + U;                                                \
-      if (i < n) {                                                         \
-        wait_vm<LPP * (NB - 1)>();                                         \
-        consume(i, std::integral_constant<int, (U < NB ? U : 0)>{});       \
-      }                                                                    \
-    }
-    DD_STREAM_STEP(0)
-    DD_STREAM_STEP(1)
-    DD_STREAM_STEP(2)
-    DD_STREAM_STEP(3)
-#undef DD_STREAM_STEP
-  }
+  // Full groups of NB pairs run without guards and the last n % NB after
+  // the loop (see stream_kernel).
+  auto step = [&](int i, auto u_tag) __attribute__((always_inline)) {
+    wait_vm<LPP * (NB - 1)>();
+    consume(i, u_tag);
+  };
+  int i0 = 0;
+  for (; i0 + NB <= n; i0 += NB)
+    static_for<NB>([&](auto u) __attribute__((always_inline)) { step(i0 + decltype(u)::value, u); });
+  static_for<NB - 1>([&](auto u) __attribute__((always_inline)) {
+    if (i0 + decltype(u)::value < n) step(i0 + decltype(u)::value, u);
+  });
   wait_vm<0>();
+
+  // remove the V offsets: O^T row d of head n16 holds 1152 * (sum of that
+  // head's fp16 P over all keys, V group of d) too
+#pragma unroll
+  for (int g = 0; g < NG; ++g) psum[g] = kI8Offset * xor32_sum(xor16_sum(psum[g]));
+#pragma unroll
+  for (int md = 0; md < MD; ++md) o[md] -= psum[NG == 1 ? 0 : (16 * md) / 32];
 
   stream_epilogue<QT, D, NW>(p, s_ml, (float *)s_ring, o, m_run, lsum, w, lane, b, kh, split);
 #endif  // __HIP_DEVICE_COMPILE__
