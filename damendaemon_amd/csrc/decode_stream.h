@@ -703,21 +703,35 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
   };
 
   // Everything enters the matrix cores as fp16 (see the int8 section note):
-  // K and V bytes as exact fp16 values b + 1152, Q converted to fp16, the
+  // K and V bytes as exact fp16 values b + 1152, the query scaled by a power
+  // of two 2^-qe (chosen per head so that its largest component is about
+  // 2^14: no fp16 overflow, nothing relevant in subnormals) and rounded to
+  // fp16 -- exact for bf16 queries, whose 8-bit significands fit -- and the
   // probabilities p * v_scale as fp16.  The 1152 offsets come out of S^T
   // through the column sums of Q (qoff) and out of O^T through the column
-  // sums of the fp16 P^T operands (psum).
+  // sums of the fp16 P^T operands (psum); 2^qe goes back into the logit scale.
+  float qf[NC][8];
+  float qmax = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    after_wait(qa[c]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      qf[c][2 * j] = QT == DD_BF16 ? bf16_lo(qa[c][j]) : f16_lo(qa[c][j]);
+      qf[c][2 * j + 1] = QT == DD_BF16 ? bf16_hi(qa[c][j]) : f16_hi(qa[c][j]);
+      qmax = fmaxf(qmax, fmaxf(__builtin_fabsf(qf[c][2 * j]), __builtin_fabsf(qf[c][2 * j + 1])));
+    }
+  }
+  qmax = xor32_max(xor16_max(qmax));   // over the head's D components
+  const int qe = qmax > 0.f && __builtin_isfinite(qmax) ? __builtin_amdgcn_frexp_expf(qmax) - 15 : 0;
+  const float lscale = __builtin_ldexpf(p.scale_log2, qe);   // logit scale of the scaled query
   u32x4 qh[NC];
   float qoff[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    after_wait(qa[c]);
-    if constexpr (QT == DD_BF16) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) qh[c][j] = cvt_pk_f16(bf16_lo(qa[c][j]), bf16_hi(qa[c][j]));
-    } else {
-      qh[c] = qa[c];
-    }
+    for (int j = 0; j < 4; ++j)
+      qh[c][j] = cvt_pk_f16(__builtin_ldexpf(qf[c][2 * j], -qe), __builtin_ldexpf(qf[c][2 * j + 1], -qe));
     float qs = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) qs = dot2_f16(qh[c][j], 0x3C003C00u, qs);
@@ -792,7 +806,7 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
           qo += qoff[c];
         }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sacc[e] = (sacc[e] - qo) * (scale_of(ks8, ch, e, 0) * p.scale_log2);
+        for (int e = 0; e < 4; ++e) sacc[e] = (sacc[e] - qo) * (scale_of(ks8, ch, e, 0) * lscale);
       } else {
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
@@ -801,7 +815,7 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
           for (int e = 0; e < 4; ++e) sacc[e] += scale_of(ks8, ch, e, c) * (part[e] - qoff[c]);
         }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sacc[e] *= p.scale_log2;
+        for (int e = 0; e < 4; ++e) sacc[e] *= lscale;
       }
       float rb[4] = {0.f, 0.f, 0.f, 0.f};
       if (!FAST && p.rel) {  // workgroup-uniform

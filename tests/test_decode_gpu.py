@@ -163,6 +163,34 @@ def test_int8_pages(group, qdtype):
     check(run_case(case), oracle_case(case), torch.int8)
 
 
+@pytest.mark.parametrize('qmag', [3e4, 1e-5])
+@pytest.mark.parametrize('group', [128, 32])
+def test_int8_query_and_value_ranges(qmag, group):
+    """The int8 path feeds the matrix cores fp16: queries far outside fp16's
+    comfortable range (x3e4, x1e-5, softmax scale compensating), and V rows
+    whose magnitudes span 1e-6 .. 1e4 within one sequence (so p * v_scale
+    spans ~2^33), must stay inside the int8 bound."""
+    case = paged_decode_case([7, 200, 1500], 16, 4, 128, torch.float32, seed=int(qmag * 10) + group, nan_fill=False)
+    g = torch.Generator().manual_seed(group)
+    mag = torch.exp(torch.empty(case['cache_v'].shape[:3] + (1,)).uniform_(math.log(1e-6), math.log(1e4),
+                                                                             generator=g))
+    case['cache_v'] = case['cache_v'] * mag
+    qk, ks = oracle.quantize_q8(case['cache_k'], group)
+    qv, vs = oracle.quantize_q8(case['cache_v'], group)
+    query = (case['query'] * qmag).to(torch.bfloat16)
+    scale = 128 ** -.5 / qmag
+    case.update(cache_k=qk, cache_v=qv, k_scale=ks, v_scale=vs, query=query)
+    out = run_case(case, scale=scale)
+    exp = oracle_case(case, scale=scale)
+    # the outputs span the V magnitudes: the int8 bound is taken relative to
+    # each row's largest value, plus the bf16 output's own half ulp (2^-9)
+    a = out.cpu().double()
+    assert torch.isfinite(a).all()
+    row_mag = exp.abs().amax(dim=-1, keepdim=True).clamp_min(1e-300)
+    err = ((a - exp).abs() / row_mag).max().item()
+    assert err <= 5e-3 + 2 ** -9, f'max error {err:.3e} of the row magnitude'
+
+
 def test_int8_dim256_group32():
     case = paged_decode_case([40, 900, 3000], 16, 2, 256, torch.float32, seed=3)
     qk, ks = oracle.quantize_q8(case['cache_k'], 32)
