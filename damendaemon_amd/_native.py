@@ -96,3 +96,48 @@ def require_device(*tensors):
         if t is not None and t.device.type != 'cuda':
             raise ValueError('damendaemon_amd kernels need tensors on the GPU '
                              '(there is no CPU path)')
+
+
+class _Staging:
+    """Pinned host buffers for the small per-call uploads (segment metadata,
+    prefill plans), reused round-robin instead of pinning fresh memory on
+    every call: pinning costs far more than the copy.  Each slot remembers
+    the event of its last copy and waits for it before being rewritten."""
+
+    SLOTS = 8
+
+    def __init__(self):
+        self._slots = {}   # device index -> list of [pinned uint8 buffer, event or None]
+        self._next = {}
+
+    def upload(self, host, device):
+        """Asynchronous copy of the contiguous CPU tensor ``host`` to ``device``
+        on the current stream; returns the device tensor."""
+        host = host.contiguous()
+        nbytes = host.numel() * host.element_size()
+        dev = torch.device(device)
+        index = dev.index if dev.index is not None else torch.cuda.current_device()
+        slots = self._slots.setdefault(index, [[None, None] for _ in range(self.SLOTS)])
+        k = self._next.get(index, 0)
+        self._next[index] = (k + 1) % self.SLOTS
+        slot = slots[k]
+        if slot[1] is not None:
+            slot[1].synchronize()
+        if slot[0] is None or slot[0].numel() < nbytes:
+            slot[0] = torch.empty(max(nbytes, 4096), dtype=torch.uint8, pin_memory=True)
+        staged = slot[0][:nbytes].view(host.dtype).view(host.shape)
+        staged.copy_(host)
+        out = torch.empty(host.shape, dtype=host.dtype, device=dev)
+        out.copy_(staged, non_blocking=True)
+        if slot[1] is None:
+            slot[1] = torch.cuda.Event()
+        slot[1].record(torch.cuda.current_stream(dev))
+        return out
+
+
+_staging = _Staging()
+
+
+def upload(host, device):
+    """Copy a small CPU tensor to the GPU through the reusable pinned buffers."""
+    return _staging.upload(host, device)

@@ -47,7 +47,7 @@ def pack_batch(lengths, starts, slots, page_table=None, page_size=16, device='cu
     pages = sum(-(-(s + l) // page_size) for s, l in zip(starts, lengths))
     dev = torch.device(device)
     meta = torch.tensor([lengths, starts, slots], dtype=torch.int64).reshape(3, n)
-    meta = meta.pin_memory().to(dev, non_blocking=True) if dev.type == 'cuda' else meta.to(dev)
+    meta = _native.upload(meta, dev) if dev.type == 'cuda' else meta.to(dev)
     _native.require_device(meta, page_table)
     if page_table is not None and (page_table.dtype != torch.int32 or not page_table.is_contiguous()):
         raise ValueError('page table must be a contiguous int32 matrix')

@@ -90,7 +90,7 @@ def prefill_attention(query, cache_k, cache_v, packed, page_table, window=0, sca
         plan = prefill_plan(packed.lengths[a:b], packed.starts[a:b], H, cache_k.shape[1], D, window)
         if len(plan) == 0:
             return out
-        plan_dev = torch.from_numpy(plan).pin_memory().to(q.device, non_blocking=True)
+        plan_dev = _native.upload(torch.from_numpy(plan), q.device)
         plan_len = len(plan)
     call('dd_prefill_attention', ptr(q), ptr(cache_k), ptr(cache_v), DTYPE_CODES[q.dtype],
          ptr(packed.cu_seqlens[a:]), ptr(packed.context_lens[a:]), ptr(packed._meta[2, a:]), b - a, max_len, max_context,
