@@ -262,18 +262,28 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(dst + j * 1024), 16, v_dma_lane, 64 * j, 0, 0);
   };
   const unsigned v_base = lds_addr(s_v);
-  // bf16 V tile kt -> fp16 in place (16 contiguous bytes per lane)
-  auto convert_v = [&](int kt) __attribute__((always_inline)) {
+  // bf16 V tile kt -> fp16 in place (16 contiguous bytes per lane), in two
+  // halves: the reads, and after other work the conversion and writes
+  auto convert_v_read = [&](int kt, u32x4 (&x)[VJ]) __attribute__((always_inline)) {
     if constexpr (DT == DD_BF16) {
       const unsigned base = v_base + ((kt - kt_first) % NVS) * PLANE + 16u * tid;
-      u32x4 x[VJ];
 #pragma unroll
       for (int j = 0; j < VJ; ++j) x[j] = lds_read128(base, j * 16 * NT);
+    }
+  };
+  auto convert_v_write = [&](int kt, u32x4 (&x)[VJ]) __attribute__((always_inline)) {
+    if constexpr (DT == DD_BF16) {
+      const unsigned base = v_base + ((kt - kt_first) % NVS) * PLANE + 16u * tid;
 #pragma unroll
       for (int j = 0; j < VJ; ++j) lgkm_wait(x[j], 0);
 #pragma unroll
       for (int j = 0; j < VJ; ++j) lds_write128(base, j * 16 * NT, bf16x8_to_f16x8(x[j]));
     }
+  };
+  auto convert_v = [&](int kt) __attribute__((always_inline)) {
+    u32x4 x[VJ];
+    convert_v_read(kt, x);
+    convert_v_write(kt, x);
   };
 
   // ---- S^T of one tile: two 32-key blocks ----
@@ -409,9 +419,14 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   };
 
   // ---- vector phase of step kt: P(kt+1) from S(kt+1); V(kt+1) to fp16 in
-  // its LDS slot; the page numbers of the next step's loads ----
-  auto valu_phase = [&](int kt, f32x16 (&s)[2], u32x4 (&pp)[2][2])
+  // its LDS slot; the page number of the next step's loads.  The LDS reads
+  // go first and the LDS writes mid-way, so that their latencies overlap
+  // the softmax ----
+  auto valu_phase = [&](int kt, f32x16 (&s)[2], u32x4 (&pp)[2][2], int &pk)
       __attribute__((always_inline)) {
+    u32x4 x[VJ];
+    convert_v_read(kt + 1, x);
+    pk = lookup(kt + NKS + 1, k_chunk);
     mask(kt + 1, s);
     float m = kNegInf;
 #pragma unroll
@@ -419,11 +434,13 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
     const float mu = softmax_begin(xor32_max(m));
     float lsum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) softmax_pair(s, i, mu, pp, lsum);
+    for (int i = 0; i < 8; ++i) softmax_pair(s, i, mu, pp, lsum);
+    // V(kt+1) of every wave landed before the previous barrier
+    convert_v_write(kt + 1, x);
+#pragma unroll
+    for (int i = 8; i < 16; ++i) softmax_pair(s, i, mu, pp, lsum);
     l_part += lsum;
-    // V(kt+1) of every wave landed before the previous barrier; this wave's
-    // K(kt+2) and V(kt+2) land before the next one
-    convert_v(kt + 1);
+    // this wave's K(kt+2) and V(kt+2) land before the next barrier
     vm_wait<VMW>();
   };
 
@@ -486,8 +503,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
       issue_k(kt + NKS, pku);
       issue_v(kt + NKS, pku);
     });
-    valu_phase(kt, s, pp);
-    pk = lookup(kt + NKS + 1, k_chunk);
+    valu_phase(kt, s, pp, pk);
     lgkm_drain();
     barrier();
   }
