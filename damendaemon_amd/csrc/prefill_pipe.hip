@@ -12,8 +12,11 @@
 //
 // Step structure.  Step t of a wave issues the MFMAs of S(t+1) = K(t+1) Q^T
 // and O += V(t)^T P(t) back to back, then the vector work of tile t+1:
-// mask, column max, exponentials into the fp16 P^T operands, row sums, and
-// the in-place fp16 conversion of V(t+1); one barrier per step.  The two
+// mask, exponentials into the fp16 P^T operands, row sums, and the in-place
+// fp16 conversion of V(t+1); one barrier per step.  The exponentials use
+// the column's running offset without a max over the tile; only a tile
+// that pushes a probability past fp16's range (or a column's first tile)
+// takes the max and moves the offset.  The two
 // waves of a SIMD drift apart within a step, so one's vector work fills the
 // other's matrix-core phase (measured: interleaving the two inside a wave
 // by hand was slower).
@@ -421,24 +424,37 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   // ---- vector phase of step kt: P(kt+1) from S(kt+1); V(kt+1) to fp16 in
   // its LDS slot; the page number of the next step's loads.  The LDS reads
   // go first and the LDS writes mid-way, so that their latencies overlap
-  // the softmax ----
+  // the softmax.
+  // The exponentials are taken against the column's current offset without
+  // a max over the tile: while no score exceeds the running max by 16 (in
+  // the exp2 domain) every probability is a finite fp16 value and nothing
+  // moves.  A column without a running max yet (offset -inf) or a
+  // probability past fp16's range shows up as a non-finite row sum; then
+  // the wave redoes the tile with the tile's max (moving the offset and
+  // rescaling O and l as usual) ----
   auto valu_phase = [&](int kt, f32x16 (&s)[2], u32x4 (&pp)[2][2], int &pk)
       __attribute__((always_inline)) {
     u32x4 x[VJ];
     convert_v_read(kt + 1, x);
     pk = lookup(kt + NKS + 1, k_chunk);
     mask(kt + 1, s);
-    float m = kNegInf;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) max_part(s, i, m);
-    const float mu = softmax_begin(xor32_max(m));
+    const float mu0 = m_run * sc;
     float lsum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) softmax_pair(s, i, mu, pp, lsum);
+    for (int i = 0; i < 8; ++i) softmax_pair(s, i, mu0, pp, lsum);
     // V(kt+1) of every wave landed before the previous barrier
     convert_v_write(kt + 1, x);
 #pragma unroll
-    for (int i = 8; i < 16; ++i) softmax_pair(s, i, mu, pp, lsum);
+    for (int i = 8; i < 16; ++i) softmax_pair(s, i, mu0, pp, lsum);
+    if (__builtin_amdgcn_ballot_w64(!(lsum <= 3.0e38f))) {
+      float m = kNegInf;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) max_part(s, i, m);
+      const float mu = softmax_begin(xor32_max(m));
+      lsum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) softmax_pair(s, i, mu, pp, lsum);
+    }
     l_part += lsum;
     // this wave's K(kt+2) and V(kt+2) land before the next barrier
     vm_wait<VMW>();

@@ -63,6 +63,30 @@ def test_prefill_window(window):
     check(out, exp)
 
 
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize('slope', [0.5, -0.5, 0.02])
+def test_prefill_running_max_moves(dtype, slope):
+    """Scores that rise (or fall) steeply along the keys: with slope 0.5 every
+    64-key tile exceeds the running max by far more than the fp16 range of the
+    probabilities, so each tile takes the kernel's re-offset path; slope 0.02
+    moves the max a little on every tile."""
+    lengths, starts = [64, 200], [0, 700]
+    heads, kvh, dim = 8, 2, 128
+    case, q, slots = build(lengths, starts, heads, kvh, dim, dtype, seed=77, nan_fill=False)
+    u = torch.ones(dim) / dim ** 0.5
+    g = torch.Generator().manual_seed(78)
+    q = (4 * u + 0.05 * torch.randn(sum(lengths), heads, dim, generator=g)).to(dtype)
+    ck, table = case['cache_k'], case['page_table']
+    for slot, (n, st) in enumerate(zip(lengths, starts)):
+        for j in range(st + n):
+            page = int(table[slot, j // 16])
+            ck[page, :, j % 16] = (slope * j * u + 0.05 * torch.randn(kvh, dim, generator=g)).to(dtype)
+    packed = packing.pack_batch(lengths, starts, slots, table.to(DEV))
+    out = ragged.prefill_attention(q.to(DEV), ck.to(DEV), case['cache_v'].to(DEV), packed, table.to(DEV))
+    exp = O.prefill_attention(q, ck, case['cache_v'], lengths, starts, slots, table)
+    check(out, exp)
+
+
 def test_mixed_batch_end_to_end():
     """Config C4 at reduced size: pack on the GPU, write the new K/V into the pages, attend."""
     rng = random.Random(4)
