@@ -132,7 +132,8 @@ def cpu_baseline(case, budget_s=20.0):
 def run_probes():
     """Build damendaemon_amd/probes/overlap.hip (hipcc, gfx950) into a temporary
     directory and run it: exp / fma / MFMA issue rates, LDS read bandwidth and
-    the best-case prefill tile-step (one JSON line each)."""
+    the best-case prefill tile-steps, MFMA/VALU co-issue and the shader
+    clock (one JSON line each)."""
     import subprocess
     import tempfile
     src = os.path.join(ROOT, 'damendaemon_amd', 'probes', 'overlap.hip')
