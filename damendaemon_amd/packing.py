@@ -8,6 +8,7 @@ array of (length, start, slot) per segment and the GPU expands it.
 """
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from . import _native
@@ -39,14 +40,18 @@ def pack_batch(lengths, starts, slots, page_table=None, page_size=16, device='cu
     scheduler's own lists).  With a ``page_table`` the slot map and the page
     gather lists are produced too.
     """
-    lengths, starts, slots = list(map(int, lengths)), list(map(int, starts)), list(map(int, slots))
-    n = len(lengths)
-    if len(starts) != n or len(slots) != n or any(x < 0 for x in lengths + starts) or page_size <= 0:
+    try:
+        host = np.array((lengths, starts, slots), dtype=np.int64)
+    except (TypeError, ValueError, OverflowError):
+        raise ValueError('invalid packing request') from None
+    if host.ndim != 2 or page_size <= 0 or (host[:2] < 0).any():
         raise ValueError('invalid packing request')
-    total = sum(lengths)
-    pages = sum(-(-(s + l) // page_size) for s, l in zip(starts, lengths))
+    n = host.shape[1]
+    lengths, starts, slots = host.tolist()
+    total = int(host[0].sum())
+    pages = int(((host[0] + host[1] + (page_size - 1)) // page_size).sum())
     dev = torch.device(device)
-    meta = torch.tensor([lengths, starts, slots], dtype=torch.int64).reshape(3, n)
+    meta = torch.from_numpy(host)
     meta = _native.upload(meta, dev) if dev.type == 'cuda' else meta.to(dev)
     _native.require_device(meta, page_table)
     if page_table is not None and (page_table.dtype != torch.int32 or not page_table.is_contiguous()):
