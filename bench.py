@@ -43,17 +43,32 @@ def algorithmic_bytes(case, kv_bytes_per_token_head):
     return ctx * KH * kv_bytes_per_token_head + q_o + pages * 4
 
 
-def source_digest():
-    """sha256 over the HIP sources (csrc/*.hip, *.h, sorted by name): ties a
-    profile summary to the kernels it measured."""
+# Kernel families and the sources each one is compiled from (besides common.h
+# and the public header): a profile summary records the digest of its family.
+DIGEST_FAMILIES = {
+    'decode': ('decode', 'q8.h'),
+    'prefill': ('prefill',),
+    'rope': ('rope',),
+    'copy': ('copy',),
+}
+
+
+def source_digest(family=None):
+    """sha256 over the HIP sources of one kernel family (csrc/ files whose name
+    starts with one of its prefixes, plus common.h and the public header), or
+    over every source when family is None: ties a profile summary to the
+    kernels it measured."""
     import hashlib
     csrc = os.path.join(ROOT, 'damendaemon_amd', 'csrc')
+    prefixes = DIGEST_FAMILIES[family] if family else ('',)
     h = hashlib.sha256()
-    for name in sorted(os.listdir(csrc)):
-        if name.endswith(('.hip', '.h')):
-            h.update(name.encode())
-            with open(os.path.join(csrc, name), 'rb') as f:
-                h.update(f.read())
+    files = [os.path.join(csrc, n) for n in sorted(os.listdir(csrc))
+             if n.endswith(('.hip', '.h')) and (n == 'common.h' or n.startswith(prefixes))]
+    files.append(os.path.join(ROOT, 'include', 'damendaemon_amd.h'))
+    for path in files:
+        h.update(os.path.basename(path).encode())
+        with open(path, 'rb') as f:
+            h.update(f.read())
     return h.hexdigest()[:16]
 
 
@@ -70,7 +85,7 @@ def measured_traffic(summary):
         if ':' in line and not line.startswith(('#', '|', ' ')):
             key, _, val = line.partition(':')
             fields[key.strip()] = val.strip().strip('`')
-    if fields.get('source_digest') != source_digest() or 'traffic_bytes_per_launch' not in fields:
+    if fields.get('source_digest') != source_digest('decode') or 'traffic_bytes_per_launch' not in fields:
         return None
     return int(fields['traffic_bytes_per_launch'])
 
@@ -150,7 +165,7 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=50)
     ap.add_argument('--warmup', type=int, default=5)
-    ap.add_argument('--config', default='c2', choices=['c2', 'c3', 'c4', 'c5'])
+    ap.add_argument('--config', default='c2', choices=['c2', 'c3', 'c4', 'c5', 'rope', 'copy'])
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--copy-probe', action='store_true',
                     help='only run 1 GiB device-to-device copies (calibrates rocprofv3 FETCH/WRITE_SIZE)')
@@ -177,6 +192,10 @@ def main():
     torch.cuda.set_device(0)
     if args.config == 'c4':
         return bench_mixed(args, dev)
+    if args.config == 'rope':
+        return bench_rope(args, dev)
+    if args.config == 'copy':
+        return bench_copy(args, dev)
     case, workload, dtype, nbytes = build_case(args.config, dev)
     launch = kernels.prepare_attention(case['query'], case['cache_k'], case['cache_v'], case['positions'],
                                        case['slots'], page_table=case['page_table'],
@@ -235,7 +254,7 @@ def main():
                    'step_hbm_gbps': nbytes / (ms_per_step * 1e-3) / 1e9},
         'roofline': {'bound': 'hbm', 'achieved': achieved, 'peak': PEAK_HBM_GBPS, 'unit': 'GB/s',
                      'frac': achieved / PEAK_HBM_GBPS, 'traffic': measured_traffic(f'decode_{args.config}_pmc'),
-                     'algorithmic_bytes': nbytes, 'source_digest': source_digest()},
+                     'algorithmic_bytes': nbytes, 'source_digest': source_digest('decode')},
         'cpu_baseline': None if args.no_cpu_baseline else cpu_baseline(case),
     }
     print(json.dumps(line), flush=True)
@@ -294,6 +313,85 @@ def bench_mixed(args, dev):
         'roofline': {'bound': 'mfma', 'achieved': tflops, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
                      'frac': tflops / PEAK_BF16_TFLOPS, 'traffic': None},
         'cpu_baseline': None}), flush=True)
+
+
+def _event_mean_ms(fn, steps, warmup):
+    """Mean duration of fn's GPU work, HIP events on the launch stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    for a, b in events:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return statistics.mean(a.elapsed_time(b) for a, b in events)
+
+
+def _hbm_line(metric, unit_value, unit, ms, nbytes, steps, warmup, dtype, workload, family, extra=None):
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    return {'metric': metric, 'value': unit_value / (ms * 1e-3), 'unit': unit, 'n_gpus': 1, 'steps': steps,
+            'warmup': warmup, 'ms_per_step': ms, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
+            'dtype': dtype, 'data': 'synthetic (seeded)', 'config': dict({'workload': workload}, **(extra or {})),
+            'roofline': {'bound': 'hbm', 'achieved': achieved, 'peak': PEAK_HBM_GBPS, 'unit': 'GB/s',
+                         'frac': achieved / PEAK_HBM_GBPS, 'traffic': None, 'algorithmic_bytes': nbytes,
+                         'source_digest': source_digest(family)},
+            'cpu_baseline': None}
+
+
+def bench_rope(args, dev):
+    """Fused RoPE + paged K/V write (kernels.rope_batch, reference kernels.py:271-340) on the
+    C4 packed batch: 4,216 tokens, H32/KH8/D128 bf16, page 16."""
+    from damendaemon_amd import kernels, packing, workloads
+    case = workloads.config_c4(device=dev)
+    table, ck, cv = case['page_table'], case['cache_k'], case['cache_v']
+    packed = packing.pack_batch(case['lengths'], case['starts'], case['seg_slots'], table)
+    T, H, KH, D = packed.total_tokens, 32, 8, 128
+    g = torch.Generator(device=dev).manual_seed(7)
+    qkv = torch.randn((T, (H + 2 * KH) * D), generator=g, device=dev).to(torch.bfloat16)
+    positions_max = max(s + n for s, n in zip(case['starts'], case['lengths']))
+    ang = torch.arange(positions_max, device=dev, dtype=torch.float32)[:, None] * \
+        torch.pow(10000.0, -torch.arange(0, D, 2, device=dev, dtype=torch.float32) / D)[None, :]
+    cos = torch.cat([ang.cos(), ang.cos()], 1).to(torch.bfloat16)
+    sin = torch.cat([ang.sin(), ang.sin()], 1).to(torch.bfloat16)
+
+    def step():
+        kernels.rope_batch(qkv, cos, sin, packed.positions, packed.slot_ids, ck, cv, H, page_table=table)
+
+    ms = _event_mean_ms(step, args.steps, args.warmup)
+    # per token: qkv row read, cos + sin rows read, Q row written, K and V rows written into the
+    # pages, position + slot ids, one page-table entry
+    per_token = (H + 2 * KH) * D * 2 + 2 * D * 2 + H * D * 2 + 2 * KH * D * 2 + 16 + 4
+    line = _hbm_line('fused RoPE + paged K/V write: tokens/s and achieved HBM GB/s (% peak), 1 MI355X', T,
+                     'tokens/s', ms, T * per_token, args.steps, args.warmup, 'bf16',
+                     'C4 packed batch through rope_batch: 4,216 tokens (8 x 512 prefill + 120 decode), '
+                     'H32/KH8/D128, rotary dim 128, page 16', 'rope', {'bytes_per_token': per_token})
+    print(json.dumps(line), flush=True)
+
+
+def bench_copy(args, dev):
+    """copy_pages gather and restore (paged_kernels.copy_pages, reference paged_kernels.py:8-47) of one
+    32,768-token slot of the C5 geometry: KH2/D256 bf16, pages scattered over the pool."""
+    from damendaemon_amd import paged_kernels
+    KH, D, P, tokens = 2, 256, 16, 32768
+    pages = tokens // P
+    cap = pages + pages // 4
+    g = torch.Generator(device=dev).manual_seed(9)
+    cache = torch.randn((2, cap, KH, P, D), generator=g, device=dev).to(torch.bfloat16)
+    perm = torch.randperm(cap, generator=torch.Generator().manual_seed(9))[:pages]
+    table = perm.to(torch.int32).reshape(1, pages).to(dev)
+    dense = paged_kernels.copy_pages(cache, table, 0, tokens)
+    gather_ms = _event_mean_ms(lambda: paged_kernels.copy_pages(cache, table, 0, tokens), args.steps, args.warmup)
+    restore_ms = _event_mean_ms(lambda: paged_kernels.copy_pages(cache, table, 0, tokens, dense), args.steps,
+                                args.warmup)
+    nbytes = 2 * dense.numel() * dense.element_size() + pages * 4   # read + write, plus page-table entries
+    line = _hbm_line('copy_pages gather: tokens/s and achieved HBM GB/s (% peak), 1 MI355X', tokens, 'tokens/s',
+                     gather_ms, nbytes, args.steps, args.warmup, 'bf16',
+                     'one 32,768-token slot, KH2/D256 bf16, page 16, pages scattered (C5 geometry)', 'copy',
+                     {'restore_ms': restore_ms,
+                      'restore_hbm_gbps': nbytes / (restore_ms * 1e-3) / 1e9})
+    print(json.dumps(line), flush=True)
 
 
 if __name__ == '__main__':

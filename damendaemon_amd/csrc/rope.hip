@@ -13,8 +13,22 @@
 // and sum here is a separate correctly-rounded fp32 operation (no FMA
 // contraction), as in the reference's enable_fp_fusion=False build.
 //
-// One wavefront per (token, head); lanes stride over the channels.
+// Two kernels.  rope_vec_kernel, for full-width rotation of 16-bit rows into a
+// cache of the same dtype at head sizes 64/128/256 (the common case): one
+// workgroup per token, so the position, slot and page lookups are done once
+// per token; a lane owns 8 consecutive channels of a head (16-byte loads and
+// stores), and the rotate-half partner channels come from the lane D/16 away
+// within the head's lane group.  rope_kernel, for everything else: one
+// wavefront per (token, head), lanes striding over the channels.  Both apply
+// the same per-element sequence of fp32 operations and fp16 roundings.
 #include "common.h"
+
+// Every fp16 rounding below takes an fp32 value that has already been
+// rounded: the reference rounds a product to fp32 and then to fp16, and the
+// compiler would otherwise fold "fp32 multiply, then convert to fp16" into
+// one mixed-precision FMA (v_fma_mix*) that rounds the exact product once --
+// a different result whenever the fp32 product is an fp16 tie.
+#pragma clang fp contract(off)
 
 namespace {
 
@@ -26,7 +40,10 @@ DD_DEV float load_code(const void *p, long i, int code) {
   }
 }
 
-DD_DEV float round_f16(float x) { return half_bits_to_float(float_to_f16_bits(x)); }
+DD_DEV float round_f16(float x) {
+  asm("" : "+v"(x));   // x is an fp32 value here, not an expression the conversion may absorb
+  return half_bits_to_float(float_to_f16_bits(x));
+}
 
 struct RopeParams {
   const void *x;
@@ -123,6 +140,140 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeParams p) {
   }
 }
 
+// 16-bit <-> fp32 for the 16-bit row formats (bit patterns in the low half)
+template <int XT>
+DD_DEV float h2f(unsigned h) {
+  if constexpr (XT == DD_BF16) return __uint_as_float(h << 16);
+  else return half_bits_to_float((unsigned short)h);
+}
+template <int XT>
+DD_DEV unsigned f2h(float x) {
+  if constexpr (XT == DD_BF16) return float_to_bf16_bits(x);
+  else return float_to_f16_bits(x);
+}
+
+template <int XT, int CS>
+__global__ __launch_bounds__(256) void rope_vec_kernel(RopeParams p) {
+  const long b = blockIdx.x;
+  const int D = p.D;
+  const int lph = D / 8;                 // lanes per head
+  const int hl = threadIdx.x % lph;      // lane within the head's group
+  const int hpp = 256 / lph;             // heads per pass of the workgroup
+  const int heads = p.H + 2 * p.KH;
+  const long pos = p.pos[b];
+  const long slot = p.slots[b];
+  long cslot = slot, cpos = pos;
+  if (p.table) {
+    const long entry = pos / p.C;
+    cslot = (slot >= 0 && slot < p.table_rows && entry < p.table_w) ? p.table[slot * p.table_w + entry] : -1;
+    cpos = pos % p.C;
+  }
+  const bool cache_ok = cslot >= 0 && cslot < p.capacity;
+  const int j0 = 8 * hl;
+  // cos / sin of this lane's channels at the token's position
+  float c[8], sn[8];
+  if constexpr (CS == DD_F32) {
+    const f32x4 *cp = (const f32x4 *)((const float *)p.cos + pos * D + j0);
+    const f32x4 *sp = (const f32x4 *)((const float *)p.sin + pos * D + j0);
+    const f32x4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      c[k] = c0[k];
+      c[k + 4] = c1[k];
+      sn[k] = s0[k];
+      sn[k + 4] = s1[k];
+    }
+  } else {
+    const u32x4 cw = *(const u32x4 *)((const unsigned short *)p.cos + pos * D + j0);
+    const u32x4 sw = *(const u32x4 *)((const unsigned short *)p.sin + pos * D + j0);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      c[2 * k] = h2f<CS>(cw[k] & 0xffffu);
+      c[2 * k + 1] = h2f<CS>(cw[k] >> 16);
+      sn[2 * k] = h2f<CS>(sw[k] & 0xffffu);
+      sn[2 * k + 1] = h2f<CS>(sw[k] >> 16);
+    }
+  }
+  const bool lower = hl < lph / 2;       // channels below D/2: the partner enters negated
+  for (int h = (int)threadIdx.x / lph; h < heads; h += hpp) {
+    const long base = (b * heads + h) * (long)D + j0;
+    const u32x4 xw = *(const u32x4 *)((const unsigned short *)p.x + base);
+    if (h >= p.H + p.KH) {  // value head: stored as is
+      const int kh = h - p.H - p.KH;
+      if (cache_ok) *(u32x4 *)((unsigned short *)p.cv + ((cslot * p.KH + kh) * p.C + cpos) * D + j0) = xw;
+      if (p.tv) *(u32x4 *)((unsigned short *)p.tv + (b * p.KH + kh) * (long)D + j0) = xw;
+      continue;
+    }
+    const bool is_q = h < p.H;
+    const void *wt = is_q ? p.qw : p.kw;
+    float x[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      x[2 * k] = h2f<XT>(xw[k] & 0xffffu);
+      x[2 * k + 1] = h2f<XT>(xw[k] >> 16);
+    }
+    if (wt) {
+      float ss = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) ss += x[k] * x[k];
+      for (int off = lph / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+      const float inv = 1.f / sqrtf(__fadd_rn(ss / (float)D, p.eps));
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        float v = __fmul_rn(x[k], inv);
+        if (!p.precise) v = round_f16(v);
+        v = __fmul_rn(v, load_code(wt, j0 + k, p.w_code));
+        if (!p.precise) v = round_f16(v);
+        x[k] = v;
+      }
+    }
+    float o[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float v = __shfl_xor(x[k], lph / 2, 64);
+      o[k] = lower ? -v : v;
+    }
+    u32x4 r;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      unsigned pr = 0;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int i = 2 * k + e;
+        float a = __fmul_rn(x[i], c[i]);
+        float bb = __fmul_rn(o[i], sn[i]);
+        if (!p.precise) {
+          a = round_f16(a);
+          bb = round_f16(bb);
+        }
+        pr |= f2h<XT>(__fadd_rn(a, bb)) << (16 * e);
+      }
+      r[k] = pr;
+    }
+    if (is_q) {
+      *(u32x4 *)((unsigned short *)p.q + (b * p.H + h) * (long)D + j0) = r;
+    } else {
+      const int kh = h - p.H;
+      if (cache_ok) *(u32x4 *)((unsigned short *)p.ck + ((cslot * p.KH + kh) * p.C + cpos) * D + j0) = r;
+      if (p.tk) *(u32x4 *)((unsigned short *)p.tk + (b * p.KH + kh) * (long)D + j0) = r;
+    }
+  }
+}
+
+template <int XT>
+int launch_rope_vec(const RopeParams &p, hipStream_t s) {
+  if (p.tokens > 0x7fffffffL) return DD_EUNSUPPORTED;
+  const dim3 grid((unsigned)p.tokens);
+  switch (p.cos_code) {
+    case DD_F32: hipLaunchKernelGGL((rope_vec_kernel<XT, DD_F32>), grid, dim3(256), 0, s, p); break;
+    case DD_F16: hipLaunchKernelGGL((rope_vec_kernel<XT, DD_F16>), grid, dim3(256), 0, s, p); break;
+    case DD_BF16: hipLaunchKernelGGL((rope_vec_kernel<XT, DD_BF16>), grid, dim3(256), 0, s, p); break;
+    default: return DD_EUNSUPPORTED;
+  }
+  DD_LAUNCH_CHECK();
+  return DD_OK;
+}
+
 template <int XT>
 int launch_rope(const RopeParams &p, int ct, hipStream_t s) {
   const long items = p.tokens * (p.H + 2 * p.KH);
@@ -178,6 +329,14 @@ extern "C" int dd_rope_batch(const void *qkv, int qkv_dtype, const void *cos, co
   p.precise = precise;
   p.eps = eps;
   hipStream_t s = (hipStream_t)stream;
+  // the 16-byte accesses of the vector kernel need 16-byte aligned rows
+  auto a16 = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
+  const bool aligned = a16(qkv) && a16(cos) && a16(sin) && a16(query) && a16(cache_k) && a16(cache_v) &&
+                       a16(key_out) && a16(value_out);
+  if (aligned && rotary_dim == dim && (dim == 64 || dim == 128 || dim == 256) && cache_dtype == qkv_dtype) {
+    if (qkv_dtype == DD_BF16) return launch_rope_vec<DD_BF16>(p, s);
+    if (qkv_dtype == DD_F16) return launch_rope_vec<DD_F16>(p, s);
+  }
   switch (qkv_dtype) {
     case DD_F32: return launch_rope<DD_F32>(p, cache_dtype, s);
     case DD_F16: return launch_rope<DD_F16>(p, cache_dtype, s);

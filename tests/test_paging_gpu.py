@@ -178,6 +178,57 @@ def test_rope_batch_paged_exact(dtype, dim, precise):
     assert torch.equal(dv.cpu().nan_to_num(7.), ecv.nan_to_num(7.))
 
 
+@pytest.mark.parametrize('cos_dtype', [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize('precise', [True, False])
+def test_rope_batch_c4_batch_exact(cos_dtype, precise):
+    """The C4 packed batch (4,216 tokens, H32/KH8/D128 bf16, page 16) through the
+    per-token vector kernel, bit-exact against the oracle."""
+    from damendaemon_amd.workloads import config_c4
+    case = config_c4(device='cpu')
+    packed = packing.pack_batch(case['lengths'], case['starts'], case['seg_slots'], case['page_table'].to(DEV))
+    T, H, KH, D = packed.total_tokens, 32, 8, 128
+    g = torch.Generator().manual_seed(11)
+    qkv = torch.randn((T, (H + 2 * KH) * D), generator=g).to(torch.bfloat16)
+    ang = torch.randn((8200, D // 2), generator=g) * 3
+    ang = torch.cat((ang, ang), -1)
+    cos, sin = ang.cos().to(cos_dtype), ang.sin().to(cos_dtype)
+    ck, cv = case['cache_k'], case['cache_v']
+    dk, dv = ck.to(DEV), cv.to(DEV)
+    q = kernels.rope_batch(qkv.to(DEV), cos.to(DEV), sin.to(DEV), packed.positions, packed.slot_ids, dk, dv, H,
+                           precise=precise, page_table=case['page_table'].to(DEV))
+    eq, eck, ecv, _, _ = O.rope_batch(qkv, cos, sin, packed.positions.cpu(), packed.slot_ids.cpu(), ck, cv, H,
+                                      precise=precise, page_table=case['page_table'])
+    assert torch.equal(q.cpu(), eq)
+    assert torch.equal(dk.cpu(), eck) and torch.equal(dv.cpu(), ecv)
+
+
+@pytest.mark.parametrize('normalized', [False, True])
+def test_rope_batch_d256_bf16_tables(normalized):
+    """Head size 256, bf16 rows and bf16 cos/sin tables, slotted cache."""
+    g = torch.Generator().manual_seed(256 + normalized)
+    batch, heads, kvh, dim, context = 6, 8, 2, 256, 300
+    pos = torch.tensor([0, 1, 17, 150, 298, 299])
+    slots = torch.tensor([1, 0, 2, 3, 0, 1])
+    qkv = torch.randn((batch, (heads + 2 * kvh) * dim), generator=g).to(torch.bfloat16)
+    cos = torch.randn((context, dim), generator=g).to(torch.bfloat16)
+    sin = torch.randn_like(cos)
+    qw = torch.randn(dim, generator=g).to(torch.bfloat16) if normalized else None
+    kw = torch.randn(dim, generator=g).to(torch.bfloat16) if normalized else None
+    ck = torch.zeros((4, kvh, context, dim), dtype=torch.bfloat16)
+    cv = torch.zeros_like(ck)
+    dk, dv = ck.to(DEV), cv.to(DEV)
+    dev = lambda t: None if t is None else t.to(DEV)
+    q, k, v = kernels.rope_batch(qkv.to(DEV), cos.to(DEV), sin.to(DEV), pos.to(DEV), slots.to(DEV), dk, dv, heads,
+                                 dev(qw), dev(kw), materialize=True)
+    eq, eck, ecv, ek, ev = O.rope_batch(qkv, cos, sin, pos, slots, ck, cv, heads, qw, kw)
+    if normalized:
+        torch.testing.assert_close(q.cpu().float(), eq.float(), atol=4e-2, rtol=1e-2)
+        torch.testing.assert_close(dk.cpu().float(), eck.float(), atol=4e-2, rtol=1e-2)
+    else:
+        assert torch.equal(q.cpu(), eq) and torch.equal(dk.cpu(), eck) and torch.equal(k.cpu(), ek)
+    assert torch.equal(dv.cpu(), ecv) and torch.equal(v.cpu(), ev)
+
+
 @pytest.mark.parametrize('dim', [64, 96, 128])
 @pytest.mark.parametrize('normalized', [False, True])
 def test_rope_batch_slotted_qk_norm(dim, normalized):
