@@ -229,6 +229,27 @@ def test_rope_batch_d256_bf16_tables(normalized):
     assert torch.equal(dv.cpu(), ecv) and torch.equal(v.cpu(), ev)
 
 
+def test_rope_batch_unaligned_rows():
+    """Rows that do not start on a 16-byte boundary take the per-(token, head) kernel."""
+    g = torch.Generator().manual_seed(77)
+    T, heads, kvh, dim, context = 7, 4, 2, 128, 64
+    width = (heads + 2 * kvh) * dim
+    flat = torch.randn(T * width + 1, generator=g).to(torch.bfloat16)
+    pos = torch.tensor([0, 3, 17, 40, 63, 5, 9])
+    slots = torch.tensor([0, 1, 0, 1, 0, 1, 1])
+    cos = torch.randn((context, dim), generator=g)
+    sin = torch.randn_like(cos)
+    ck = torch.zeros((2, kvh, context, dim), dtype=torch.bfloat16)
+    cv = torch.zeros_like(ck)
+    dflat = flat.to(DEV)
+    qkv_dev = dflat[1:].view(T, width)            # 2-byte offset
+    assert qkv_dev.data_ptr() % 16 != 0
+    dk, dv = ck.to(DEV), cv.to(DEV)
+    q = kernels.rope_batch(qkv_dev, cos.to(DEV), sin.to(DEV), pos.to(DEV), slots.to(DEV), dk, dv, heads)
+    eq, eck, ecv, _, _ = O.rope_batch(flat[1:].view(T, width), cos, sin, pos, slots, ck, cv, heads)
+    assert torch.equal(q.cpu(), eq) and torch.equal(dk.cpu(), eck) and torch.equal(dv.cpu(), ecv)
+
+
 @pytest.mark.parametrize('dim', [64, 96, 128])
 @pytest.mark.parametrize('normalized', [False, True])
 def test_rope_batch_slotted_qk_norm(dim, normalized):
