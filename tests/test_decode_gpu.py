@@ -298,6 +298,27 @@ def test_scratch_bytes_partitions_rows():
     check(part, oracle_case(case), torch.float16)
 
 
+@pytest.mark.parametrize('batch', [65, 128, 200, 256, 257])
+@pytest.mark.parametrize('window', [0, 300])
+@pytest.mark.parametrize('kind', ['bf16', 'int8'])
+def test_many_sequences_launch_order(batch, window, kind):
+    """Batches across the in-kernel launch order's word boundaries (64
+    sequences per wave) and past its 256-sequence limit, with contexts that
+    end exactly on a split boundary, inside the first split and past it."""
+    g = torch.Generator().manual_seed(batch + window)
+    split_tokens = kernels._splits(3072, batch * 2)[1]
+    fixed = [1, split_tokens, 2 * split_tokens, split_tokens + 1, 3072]
+    contexts = fixed + torch.randint(1, 3073, (batch - len(fixed),), generator=g).tolist()
+    case = paged_decode_case(contexts, 8, 2, 64, torch.float32 if kind == 'int8' else torch.bfloat16,
+                             seed=batch, table_width=192)
+    if kind == 'int8':
+        qk, ks = oracle.quantize_q8(case['cache_k'], 64)
+        qv, vs = oracle.quantize_q8(case['cache_v'], 64)
+        case.update(cache_k=qk, cache_v=qv, k_scale=ks, v_scale=vs, query=case['query'].to(torch.bfloat16))
+    kw = {'window': window} if window else {}
+    check(run_case(case, **kw), oracle_case(case, **kw), torch.int8 if kind == 'int8' else torch.bfloat16)
+
+
 def test_config_c2_bf16_rows():
     """Full 64-sequence bf16 decode, every row against the oracle."""
     contexts = uniform_contexts(64, 512, 8192, 2)
