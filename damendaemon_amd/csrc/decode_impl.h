@@ -689,7 +689,7 @@ int dispatch_d(const DecodeParams &p, int D, hipStream_t s, int phase) {
       } else if (p.group == 32) {
         switch (D) {
           case 64: return launch_stream_i8<QT, 64, 2, DD_STREAM_NB64, DD_STREAM_NW64>(p, s, phase);
-          case 128: return launch_stream_i8<QT, 128, 4, DD_STREAM_NB128, DD_STREAM_NW128>(p, s, phase);
+          case 128: return launch_stream_i8<QT, 128, 4, DD_STREAM_NB128G, DD_STREAM_NW128>(p, s, phase);
           case 256: return launch_stream_i8<QT, 256, 8, DD_STREAM_NB256, DD_STREAM_NW256>(p, s, phase);
           default: break;
         }

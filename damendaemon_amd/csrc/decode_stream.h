@@ -44,6 +44,9 @@ typedef __attribute__((address_space(3))) void lds_void;
 #ifndef DD_STREAM_NB128
 #define DD_STREAM_NB128 2
 #endif
+#ifndef DD_STREAM_NB128G
+#define DD_STREAM_NB128G 2
+#endif
 #ifndef DD_STREAM_NB64
 #define DD_STREAM_NB64 4
 #endif
@@ -793,7 +796,8 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
     constexpr bool FAST = decltype(fast_tag)::value;
     // logits x = key t0 + 16 ch + 4 kg + e for head n16; y adds the exponent
     // of the key's largest V scale (the quantity the running max tracks)
-    float x[2][4], y[2][4], vsf[2][4][NG];
+    float x[2][4], y[2][4], vsf[2][4];  // vsf: V scale of the key (NG == 1 only)
+    bool lv[2][4];                        // key inside [s_lo, s_hi)
     float mx = kNegInf;
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
@@ -832,14 +836,27 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
         const int t = t0 + 16 * ch + 4 * kg + e;
         const bool live = FAST || (t >= s_lo && t < s_hi);
         const float v = FAST ? sacc[e] : sacc[e] + slope * (float)t + rb[e];
+        // Exponent of the key's largest V scale; dead keys' scales may be
+        // garbage: they enter P as 0.
         int ex = 0;
+        if constexpr (NG == 1) {
+          vsf[ch][e] = live ? scale_of(vs8, ch, e, 0) : 0.f;
+          ex = __builtin_amdgcn_frexp_expf(vsf[ch][e]);
+        } else {
+          // From the fp16 bits: scales are >= 0, so the largest bit pattern
+          // is the largest scale, and a normal one with biased exponent E
+          // lies in [2^(E-15), 2^(E-14)) (frexp's exponent E - 14).  The
+          // scales are re-read from vs8 where P is formed, not held here.
+          unsigned mh = 0;
 #pragma unroll
-        for (int g = 0; g < NG; ++g) {
-          // dead keys' scales may be garbage: they enter P as 0
-          vsf[ch][e][g] = live ? scale_of(vs8, ch, e, g) : 0.f;
-          ex = g == 0 ? __builtin_amdgcn_frexp_expf(vsf[ch][e][g])
-                      : max(ex, __builtin_amdgcn_frexp_expf(vsf[ch][e][g]));
+          for (int m = 0; m < NG / 2; ++m) {
+            const int k = (e * NG) / 2 + m;
+            const unsigned wd = vs8[ch][k >> 1][k & 1];
+            mh = max(mh, max(wd & 0xffffu, wd >> 16));
+          }
+          ex = live && mh ? (int)((mh >> 10) & 31u) - 14 : 0;
         }
+        lv[ch][e] = live;
         x[ch][e] = live ? v : kNegInf;
         y[ch][e] = live ? v + (float)ex : kNegInf;
         mx = fmaxf(mx, y[ch][e]);
@@ -876,7 +893,15 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int ch = j >> 1, e = 2 * (j & 1);
-        pb[g][j] = cvt_pk_f16(pr[ch][e] * vsf[ch][e][g], pr[ch][e + 1] * vsf[ch][e + 1][g]);
+        float s0, s1;
+        if constexpr (NG == 1) {
+          s0 = vsf[ch][e];
+          s1 = vsf[ch][e + 1];
+        } else {
+          s0 = lv[ch][e] ? scale_of(vs8, ch, e, g) : 0.f;
+          s1 = lv[ch][e + 1] ? scale_of(vs8, ch, e + 1, g) : 0.f;
+        }
+        pb[g][j] = cvt_pk_f16(pr[ch][e] * s0, pr[ch][e + 1] * s1);
         psum[g] = dot2_f16(pb[g][j], 0x3C003C00u, psum[g]);
       }
     }
