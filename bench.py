@@ -14,7 +14,7 @@ Prints ONE JSON line (the driver's contract) with:
   cpu_baseline the PyTorch CPU restatement (page gather + masked GQA SDPA,
                fp32) timed on the whole batch with every core of the
                affinity mask (a few seconds per step)
-Extra decode configurations (--config c3 / c3g32 / c5) are available for study;
+Extra decode configurations (--config c2f32 / c3 / c3g32 / c5) are available for study;
 the default line is C2.
 """
 import argparse
@@ -103,6 +103,12 @@ def build_case(name, device):
         case = workloads.quantize_pages(case, D, kv_quant)
         return case, 'C3 ragged paged decode int8 KV (fp16 scale per token-head): C2 shapes', 'int8', \
             algorithmic_bytes(case, 2 * (D + 2))
+    if name == 'c2f32':
+        import torch
+        case = workloads.config_c2(device=device, dtype=torch.float32)
+        D = case['query'].shape[-1]
+        return case, 'C2 shapes with fp32 pages (a float32 compute dtype): 64 seqs, ctx U[512,8192] seed 2, H32/KH8/D128', \
+            'f32', algorithmic_bytes(case, 2 * D * 4)
     if name == 'c3g32':
         case = workloads.config_c2(device=device)
         D = case['query'].shape[-1]
@@ -171,7 +177,7 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=50)
     ap.add_argument('--warmup', type=int, default=5)
-    ap.add_argument('--config', default='c2', choices=['c2', 'c3', 'c3g32', 'c4', 'c5', 'rope', 'copy'])
+    ap.add_argument('--config', default='c2', choices=['c2', 'c2f32', 'c3', 'c3g32', 'c4', 'c5', 'rope', 'copy'])
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--copy-probe', action='store_true',
                     help='only run 1 GiB device-to-device copies (calibrates rocprofv3 FETCH/WRITE_SIZE)')

@@ -663,8 +663,9 @@ namespace dd_decode {
 
 // Instantiated once per dtype pair in decode_<dtype>.hip.  bf16 / f16 pages
 // and int8 pages with one scale per row or per 32 channels, at D = 64, 128,
-// 256, take the streamed kernels (decode_stream.h); fp32 pages, D = 96 and
-// other int8 groupings take decode_kernel.
+// 256, and fp32 pages at D = 64, 128 take the streamed kernels
+// (decode_stream.h); D = 96, fp32 at D = 256 and other int8 groupings take
+// decode_kernel.
 template <int KVT, int QT>
 int dispatch_d(const DecodeParams &p, int D, hipStream_t s, int phase) {
   if constexpr (DD_DECODE_STREAM && KVT == QT && (KVT == DD_BF16 || KVT == DD_F16)) {
@@ -677,19 +678,28 @@ int dispatch_d(const DecodeParams &p, int D, hipStream_t s, int phase) {
       }
     }
   }
+  if constexpr (DD_DECODE_STREAM && KVT == DD_F32 && QT == DD_F32) {
+    if (p.G <= 16) {
+      switch (D) {
+        case 64: return launch_stream<DD_F32, 64, DD_STREAM_NB_F32, DD_STREAM_NW_F32>(p, s, phase);
+        case 128: return launch_stream<DD_F32, 128, DD_STREAM_NB_F32, DD_STREAM_NW_F32>(p, s, phase);
+        default: break;
+      }
+    }
+  }
   if constexpr (DD_DECODE_STREAM && KVT == DD_I8 && (QT == DD_BF16 || QT == DD_F16)) {
     if (p.G <= 16) {
       if (p.group == D) {
         switch (D) {
           case 64: return launch_stream_i8<QT, 64, 1, DD_STREAM_NB64, DD_STREAM_NW64>(p, s, phase);
-          case 128: return launch_stream_i8<QT, 128, 1, DD_STREAM_NB128, DD_STREAM_NW128>(p, s, phase);
+          case 128: return launch_stream_i8<QT, 128, 1, DD_STREAM_I8_NB128, DD_STREAM_I8_NW128>(p, s, phase);
           case 256: return launch_stream_i8<QT, 256, 1, DD_STREAM_NB256, DD_STREAM_NW256>(p, s, phase);
           default: break;
         }
       } else if (p.group == 32) {
         switch (D) {
           case 64: return launch_stream_i8<QT, 64, 2, DD_STREAM_NB64, DD_STREAM_NW64>(p, s, phase);
-          case 128: return launch_stream_i8<QT, 128, 4, DD_STREAM_NB128G, DD_STREAM_NW128>(p, s, phase);
+          case 128: return launch_stream_i8<QT, 128, 4, DD_STREAM_NB128G, DD_STREAM_I8_NW128>(p, s, phase);
           case 256: return launch_stream_i8<QT, 256, 8, DD_STREAM_NB256, DD_STREAM_NW256>(p, s, phase);
           default: break;
         }

@@ -6,15 +6,21 @@
 // T5 relative bias, window and sinks; split partials are combined by
 // merge_kernel.
 //
-// Memory path.  Each of the four waves of a workgroup (sequence, KV head,
-// split) owns every fourth 16-token chunk and a private ring of NB LDS
-// stages.  A chunk's K and V rows are copied HBM -> LDS by direct-to-LDS
+// Memory path.  Each of the NW waves of a workgroup (sequence, KV head,
+// split) owns every NW-th 16-token chunk and a private ring of NB LDS
+// stages (bf16/f16 at D = 128 and fp32: 8 waves x 1 stage, measured 1 %
+// (16-bit) and 7 % (fp32) faster on 64 ragged contexts than 4 waves x 2).  A chunk's K and V rows are copied HBM -> LDS by direct-to-LDS
 // buffer loads (no VGPRs held while in flight), marked nontemporal because
 // every KV byte is read exactly once per step.  A stage is refilled as soon
 // as its chunk has been read into registers, so NB chunks per wave are in
 // flight while one is computed.  A chunk's buffer resource covers only its
 // live rows, so rows past the split or the context, and chunks whose page is
 // unallocated, land as zeros.
+//
+// fp32 pages: Q, K, V and P enter v_mfma_f32_16x16x4_f32 unrounded (exact
+// fp32 products, one MFMA per dim of S^T and per key of O^T); O^T tile md
+// row m holds dim (D/16) m + md so that V is read 16 contiguous bytes at a
+// time.
 //
 // Math.  S^T = K Q^T with v_mfma_f32_16x16x32 (rows = the chunk's 16
 // tokens, columns = the GQA group's heads); the accumulator already has the
@@ -42,7 +48,19 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 #ifndef DD_STREAM_NB128
-#define DD_STREAM_NB128 2
+#define DD_STREAM_NB128 1
+#endif
+#ifndef DD_STREAM_NB_F32
+#define DD_STREAM_NB_F32 1
+#endif
+#ifndef DD_STREAM_NW_F32
+#define DD_STREAM_NW_F32 8
+#endif
+#ifndef DD_STREAM_I8_NB128
+#define DD_STREAM_I8_NB128 2
+#endif
+#ifndef DD_STREAM_I8_NW128
+#define DD_STREAM_I8_NW128 4
 #endif
 #ifndef DD_STREAM_NB128G
 #define DD_STREAM_NB128G 2
@@ -69,7 +87,7 @@ DD_DEV void static_for(F &&f) {
 
 
 #ifndef DD_STREAM_NW128
-#define DD_STREAM_NW128 4
+#define DD_STREAM_NW128 8
 #endif
 #ifndef DD_STREAM_NW256
 #define DD_STREAM_NW256 2
@@ -90,6 +108,17 @@ DD_DEV constexpr int stream_swz(int r) {
     return ((h & 3) << 1) | ((h >> 2) & 1);
   } else {
     return ((r & 7) << 1) | ((r >> 3) & 1);
+  }
+}
+
+// fp32 rows (4 D bytes, 16 or 32 chunks): the K operand reads 16 rows at
+// one logical chunk, so the low four chunk bits are XORed with the row.
+template <int DT, int D>
+DD_DEV constexpr int stream_swz_of(int r) {
+  if constexpr (DT == DD_F32) {
+    return r & 15;
+  } else {
+    return stream_swz<D>(r);
   }
 }
 
@@ -175,7 +204,8 @@ DD_DEV void wait_vm() {
 // Combine the waves of a workgroup and write the split's result: the
 // normalised output (one split) or the partial and its base-2 log-sum-exp.
 // `o` is this lane's O^T slice (head lane % 16, dims 16 md + 4 (lane / 16)
-// + i), `m_run` / `lsum` its head's running max and (lane-partial) sum.
+// + i; for fp32 pages dims MD (4 (lane / 16) + i) + md, MD = D / 16),
+// `m_run` / `lsum` its head's running max and (lane-partial) sum.
 // `s_o` must hold NW * 16 * (D + 4) floats and be free (no loads in flight).
 template <int DT, int D, int NW>
 DD_DEV void stream_epilogue(const DecodeParams &p, float (*s_ml)[2][16], float *s_o, const f32x4 (&o)[D / 16],
@@ -197,8 +227,17 @@ DD_DEV void stream_epilogue(const DecodeParams &p, float (*s_ml)[2][16], float *
   for (int ww = 1; ww < NW; ++ww) mm = fmaxf(mm, s_ml[ww][0][n16]);
   const float fac = m_run == kNegInf ? 0.f : fast_exp2(m_run - mm);
   if (n16 < G) {
+    if constexpr (DT == DD_F32) {
 #pragma unroll
-    for (int md = 0; md < MD; ++md) *(f32x4 *)&s_o[(w * 16 + n16) * DP + 16 * md + 4 * kg] = o[md] * fac;
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < MD / 4; ++q)
+          *(f32x4 *)&s_o[(w * 16 + n16) * DP + MD * (4 * kg + i) + 4 * q] =
+              f32x4{o[4 * q][i], o[4 * q + 1][i], o[4 * q + 2][i], o[4 * q + 3][i]} * fac;
+    } else {
+#pragma unroll
+      for (int md = 0; md < MD; ++md) *(f32x4 *)&s_o[(w * 16 + n16) * DP + 16 * md + 4 * kg] = o[md] * fac;
+    }
   }
   __syncthreads();
 
@@ -234,19 +273,21 @@ template <int DT, int D, int NB, int NW>
 __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
   // The host pass only needs the launch stub; the body is device code.
 #if __HIP_DEVICE_COMPILE__
-  constexpr int ROWB = 2 * D;        // bytes per token row
+  constexpr bool F32 = DT == DD_F32;
+  constexpr int ROWB = (F32 ? 4 : 2) * D;  // bytes per token row
   constexpr int PAGEB = 16 * ROWB;   // one 16-token chunk of K (or V)
   constexpr int IPP = PAGEB / 1024;  // DMA instructions per chunk and plane
   constexpr int STAGE = 2 * PAGEB;
   constexpr int CPR = ROWB / 16;     // 16-byte chunks per row
-  constexpr int NC = D / 32;         // S^T k-chunks
+  constexpr int NC = ROWB / 64;      // 16-byte K (and Q) operand reads per lane
   constexpr int MD = D / 16;         // O^T row tiles
   constexpr int DP = D + 4;          // padded row of the cross-wave buffer
   static_assert(IPP >= 1 && 2 * IPP * NB < 64 && NB <= 4, "vmcnt range, unrolled steps");
   static_assert((NB - 1) * STAGE + PAGEB < 65536, "ds offset range");
-  static_assert(NW * 16 * DP * 4 <= NW * NB * STAGE, "epilogue buffer fits the ring");
+  // The ring's LDS also holds the epilogue's cross-wave buffer.
+  constexpr int RING = NW * NB * STAGE > NW * 16 * DP * 4 ? NW * NB * STAGE : NW * 16 * DP * 4;
 
-  __shared__ __align__(1024) char s_ring[NW * NB * STAGE];
+  __shared__ __align__(1024) char s_ring[RING];
   __shared__ float s_ml[NW][2][16];
 
   const int lane = threadIdx.x & 63;
@@ -277,9 +318,15 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
   const long head0 = (long)b * p.H + (long)kh * G;
   const bool col_on = n16 < G;
 
-  // Q^T operand: lane (head n16, dims 8kg + 32c ..+8).
+  // Q^T operand: lane (head n16, dims 8kg + 32c ..+8); fp32: dims
+  // (D/4) kg + 4c ..+4, one v_mfma_f32_16x16x4_f32 per dim of the four.
   u32x4 qa[NC];
-  {
+  if constexpr (F32) {
+    const float *qf = (const float *)p.q;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      qa[c] = col_on ? *(const u32x4 *)(qf + (head0 + n16) * D + (D / 4) * kg + 4 * c) : u32x4{0, 0, 0, 0};
+  } else {
     const unsigned short *qb = (const unsigned short *)p.q;
 #pragma unroll
     for (int c = 0; c < NC; ++c)
@@ -294,13 +341,27 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
   for (int j = 0; j < IPP; ++j) {
     const int e = 64 * j + lane;
     const int r = e / CPR;
-    dma_off[j] = (unsigned)(r * ROWB + 16 * ((e % CPR) ^ stream_swz<D>(r)));
+    dma_off[j] = (unsigned)(r * ROWB + 16 * ((e % CPR) ^ stream_swz_of<DT, D>(r)));
   }
   unsigned k_addr[NC];
 #pragma unroll
-  for (int c = 0; c < NC; ++c) k_addr[c] = wbase + n16 * ROWB + 16 * ((4 * c + kg) ^ stream_swz<D>(n16));
+  for (int c = 0; c < NC; ++c)
+    k_addr[c] = wbase + n16 * ROWB + 16 * ((F32 ? (D / 16) * kg + c : 4 * c + kg) ^ stream_swz_of<DT, D>(n16));
+  // V^T operand.  16-bit: transposing reads (lane: 4 keys of one dim per
+  // tile).  fp32: O^T tile md, row m holds dim MD m + md, so that lane
+  // (kg, n16) reads the MD contiguous dims MD n16 .. of key 4 kg + e
+  // (MD / 4 reads of 16 bytes per key, address index e (MD / 4) + q).
   unsigned v_addr[MD];
-  {
+  if constexpr (F32) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int q = 0; q < MD / 4; ++q) {
+        const int r = 4 * kg + e;
+        v_addr[e * (MD / 4) + q] =
+            wbase + PAGEB + r * ROWB + 16 * (((MD / 4) * n16 + q) ^ stream_swz_of<DT, D>(r));
+      }
+  } else {
     const int a = lane & 15;
     const int r = 4 * kg + (a >> 2);
     const int q = a & 3;
@@ -340,7 +401,7 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
     }
     base = (long)uniform_ptr((const char *)base);
     const int live = base < 0 ? 0 : max(0, min(16, s_hi - pg * 16));
-    const long off = base < 0 ? 0 : 2 * base;
+    const long off = base < 0 ? 0 : (F32 ? 4 : 2) * base;
     const int bytes = uniform(live * ROWB);
     return ChunkRsrc{
         __builtin_amdgcn_make_buffer_rsrc((void *)uniform_ptr(kplane + off), (short)0, bytes, kRawBufferWord3),
@@ -370,22 +431,44 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
     constexpr int SOFF = decltype(stage_tag)::value * STAGE;
     const int t0 = (first + i * NW) * 16;
     u32x4 ka[NC];
-    u32x2 va[MD];
+    u32x2 va[F32 ? 1 : MD];
+    u32x4 vf[F32 ? MD : 1];
 #pragma unroll
     for (int c = 0; c < NC; ++c) ka[c] = lds_read_b128<SOFF>(k_addr[c]);
 #pragma unroll
-    for (int md = 0; md < MD; ++md) va[md] = lds_read_tr16<SOFF>(v_addr[md]);
+    for (int md = 0; md < MD; ++md) {
+      if constexpr (F32) {
+        vf[md] = lds_read_b128<SOFF>(v_addr[md]);
+      } else {
+        va[md] = lds_read_tr16<SOFF>(v_addr[md]);
+      }
+    }
     wait_lds();
 #pragma unroll
     for (int c = 0; c < NC; ++c) after_wait(ka[c]);
 #pragma unroll
-    for (int md = 0; md < MD; ++md) after_wait(va[md]);
+    for (int md = 0; md < MD; ++md) {
+      if constexpr (F32) {
+        after_wait(vf[md]);
+      } else {
+        after_wait(va[md]);
+      }
+    }
     // The stage is in registers now: refill it with chunk i + NB.
     issue(i + NB, decltype(stage_tag)::value);
 
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (F32) {
 #pragma unroll
-    for (int c = 0; c < NC; ++c) s = mfma16x16x32<DT>(ka[c], qa[c], s);
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          s = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(ka[c][q]), __uint_as_float(qa[c][q]), s, 0, 0,
+                                                   0);
+    } else {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) s = mfma16x16x32<DT>(ka[c], qa[c], s);
+    }
 
     // logits of tokens t0 + 4kg + i for head n16
     float x[4];
@@ -424,38 +507,56 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
       pr[e] = fast_exp2(x[e] - mu);
       lsum += pr[e];
     }
-    // P^T in two 16-bit parts (high, and the residual): the P.V product
-    // then carries the fp32 probabilities to ~2^-17, as the reference's fp32
-    // weighted sum does, instead of the 2^-9 of one bf16 rounding.
-    const u32x2 pb = {pack_pair<DT>(pr[0], pr[1]), pack_pair<DT>(pr[2], pr[3])};
-    u32x2 pl;
-    {
-      float r[4];
+    if constexpr (F32) {
+      // P^T stays fp32: key 4kg + e is k-index kg of the e-th MFMA of a tile.
+      if (t0 < s_lo) {   // expired keys' V must not reach the MFMA (0 * NaN)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const unsigned wd = pb[e >> 1];
-        const unsigned short hb = (unsigned short)((e & 1) ? (wd >> 16) : (wd & 0xffffu));
-        r[e] = pr[e] - (DT == DD_BF16 ? __uint_as_float((unsigned)hb << 16) : half_bits_to_float(hb));
+        for (int e = 0; e < 4; ++e)
+          if (t0 + 4 * kg + e < s_lo) {
+#pragma unroll
+            for (int q = 0; q < MD / 4; ++q) vf[e * (MD / 4) + q] = u32x4{0, 0, 0, 0};
+          }
       }
-      pl = u32x2{pack_pair<DT>(r[0], r[1]), pack_pair<DT>(r[2], r[3])};
-    }
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int md = 0; md < MD; ++md)
+          o[md] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(vf[e * (MD / 4) + md / 4][md % 4]), pr[e],
+                                                       o[md], 0, 0, 0);
+    } else {
+      // P^T in two 16-bit parts (high, and the residual): the P.V product
+      // then carries the fp32 probabilities to ~2^-17, as the reference's fp32
+      // weighted sum does, instead of the 2^-9 of one bf16 rounding.
+      const u32x2 pb = {pack_pair<DT>(pr[0], pr[1]), pack_pair<DT>(pr[2], pr[3])};
+      u32x2 pl;
+      {
+        float r[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const unsigned wd = pb[e >> 1];
+          const unsigned short hb = (unsigned short)((e & 1) ? (wd >> 16) : (wd & 0xffffu));
+          r[e] = pr[e] - (DT == DD_BF16 ? __uint_as_float((unsigned)hb << 16) : half_bits_to_float(hb));
+        }
+        pl = u32x2{pack_pair<DT>(r[0], r[1]), pack_pair<DT>(r[2], r[3])};
+      }
 
-    // Rows before the window start inside this chunk hold expired keys:
-    // their V must not reach the MFMA (0 * NaN).
-    if (t0 < s_lo) {
-      const int r0 = 4 * kg;
+      // Rows before the window start inside this chunk hold expired keys:
+      // their V must not reach the MFMA (0 * NaN).
+      if (t0 < s_lo) {
+        const int r0 = 4 * kg;
 #pragma unroll
-      for (int md = 0; md < MD; ++md) {
-        unsigned lo = va[md][0], hi = va[md][1];
-        if (t0 + r0 + 0 < s_lo) lo &= 0xffff0000u;
-        if (t0 + r0 + 1 < s_lo) lo &= 0x0000ffffu;
-        if (t0 + r0 + 2 < s_lo) hi &= 0xffff0000u;
-        if (t0 + r0 + 3 < s_lo) hi &= 0x0000ffffu;
-        va[md] = u32x2{lo, hi};
+        for (int md = 0; md < MD; ++md) {
+          unsigned lo = va[md][0], hi = va[md][1];
+          if (t0 + r0 + 0 < s_lo) lo &= 0xffff0000u;
+          if (t0 + r0 + 1 < s_lo) lo &= 0x0000ffffu;
+          if (t0 + r0 + 2 < s_lo) hi &= 0xffff0000u;
+          if (t0 + r0 + 3 < s_lo) hi &= 0x0000ffffu;
+          va[md] = u32x2{lo, hi};
+        }
       }
-    }
 #pragma unroll
-    for (int md = 0; md < MD; ++md) o[md] = mfma16x16x16<DT>(va[md], pl, mfma16x16x16<DT>(va[md], pb, o[md]));
+      for (int md = 0; md < MD; ++md) o[md] = mfma16x16x16<DT>(va[md], pl, mfma16x16x16<DT>(va[md], pb, o[md]));
+    }
   };
 
   // Prologue: NB chunks in flight, then the query operand (loaded before
