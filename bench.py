@@ -31,6 +31,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBPS = 8000.0   # MI355X HBM3E, AMD datasheet
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, AMD datasheet
+PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 MFMA, AMD datasheet
 
 
 def algorithmic_bytes(case, kv_bytes_per_token_head):
@@ -177,7 +178,7 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=50)
     ap.add_argument('--warmup', type=int, default=5)
-    ap.add_argument('--config', default='c2', choices=['c2', 'c2f32', 'c3', 'c3g32', 'c4', 'c5', 'rope', 'copy'])
+    ap.add_argument('--config', default='c2', choices=['c2', 'c2f32', 'c3', 'c3g32', 'c4', 'c4f32', 'c5', 'rope', 'copy'])
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--copy-probe', action='store_true',
                     help='only run 1 GiB device-to-device copies (calibrates rocprofv3 FETCH/WRITE_SIZE)')
@@ -204,6 +205,8 @@ def main():
     torch.cuda.set_device(0)
     if args.config == 'c4':
         return bench_mixed(args, dev)
+    if args.config == 'c4f32':
+        return bench_mixed(args, dev, torch.float32)
     if args.config == 'rope':
         return bench_rope(args, dev)
     if args.config == 'copy':
@@ -272,10 +275,13 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def bench_mixed(args, dev):
-    """Config C4: one step = GPU pack + K/V page write + mixed prefill/decode attention."""
+def bench_mixed(args, dev, dtype=torch.bfloat16):
+    """Config C4: one step = GPU pack + K/V page write + mixed prefill/decode attention
+    (c4f32: the same batch with fp32 pages, a float32 compute dtype)."""
     from damendaemon_amd import kernels, packing, ragged, workloads
-    case = workloads.config_c4(device=dev)
+    f32 = dtype == torch.float32
+    peak = PEAK_FP32_TFLOPS if f32 else PEAK_BF16_TFLOPS
+    case = workloads.config_c4(device=dev, dtype=dtype)
     table, ck, cv = case['page_table'], case['cache_k'], case['cache_v']
     lengths, starts, slots = case['lengths'], case['starts'], case['seg_slots']
     n_chunks = sum(1 for n in lengths if n > 1)
@@ -311,19 +317,21 @@ def bench_mixed(args, dev):
     decode_ms = statistics.mean(b.elapsed_time(c) for _, b, c in events)
     tflops = flops / (prefill_ms * 1e-3) / 1e12
     ctx = [s + n for s, n in zip(starts, lengths)]
-    decode_bytes = sum(ctx[n_chunks:]) * 8 * 128 * 2 * 2
+    decode_bytes = sum(ctx[n_chunks:]) * 8 * 128 * 2 * (4 if f32 else 2)
     ms = wall / args.steps * 1e3
     print(json.dumps({
         'metric': 'mixed chunked-prefill + decode attention: packed tokens/s, prefill MFMA utilisation, 1 MI355X',
         'value': sum(lengths) / (ms * 1e-3), 'unit': 'tokens/s', 'n_gpus': 1, 'steps': args.steps,
         'warmup': args.warmup, 'ms_per_step': ms, 'higher_is_better': True, 'scaling': 'weak',
-        'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic (seeded N(0,1) Q/K/V, seeded page scatter)',
-        'config': {'workload': 'C4 mixed batch: 8 x 512-token chunks on contexts U[0,4096] + 120 decodes '
+        'vs_baseline': None, 'dtype': 'f32' if f32 else 'bf16',
+        'data': 'synthetic (seeded N(0,1) Q/K/V, seeded page scatter)',
+        'config': {'workload': 'C4 mixed batch' + (' with fp32 pages' if f32 else '') +
+                               ': 8 x 512-token chunks on contexts U[0,4096] + 120 decodes '
                                'ctx U[256,8192], H32/KH8/D128, page 16 (GPU pack + page write + attention)',
                    'prefill_kernel_ms': prefill_ms, 'decode_ms': decode_ms, 'prefill_flops': flops,
                    'decode_hbm_gbps': decode_bytes / (decode_ms * 1e-3) / 1e9},
-        'roofline': {'bound': 'mfma', 'achieved': tflops, 'peak': PEAK_BF16_TFLOPS, 'unit': 'TFLOP/s',
-                     'frac': tflops / PEAK_BF16_TFLOPS, 'traffic': None},
+        'roofline': {'bound': 'mfma', 'achieved': tflops, 'peak': peak, 'unit': 'TFLOP/s',
+                     'frac': tflops / peak, 'traffic': None},
         'cpu_baseline': None}), flush=True)
 
 

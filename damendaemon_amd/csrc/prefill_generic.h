@@ -25,3 +25,7 @@ struct PrefillGenericArgs {
 };
 
 int dd_prefill_generic(const PrefillGenericArgs &args, int dtype, hipStream_t stream);
+
+// fp32 pages on the matrix cores (prefill_f32.hip): D = 64 / 128, at most 128
+// query heads per KV head; DD_EUNSUPPORTED for anything else.
+int dd_prefill_f32(const PrefillGenericArgs &args, hipStream_t stream);
