@@ -28,9 +28,9 @@ def check(actual, expected, atol=ATOL):
     return err
 
 
-def build(lengths, starts, heads, kvh, dim, dtype, seed, nan_fill=True):
+def build(lengths, starts, heads, kvh, dim, dtype, seed, nan_fill=True, page=16):
     contexts = [s + n for s, n in zip(starts, lengths)]
-    case = paged_decode_case(contexts, heads, kvh, dim, dtype, seed=seed, nan_fill=nan_fill)
+    case = paged_decode_case(contexts, heads, kvh, dim, dtype, seed=seed, nan_fill=nan_fill, page=page)
     g = torch.Generator().manual_seed(seed + 1)
     q = torch.randn(sum(lengths), heads, dim, generator=g).to(dtype)
     slots = list(range(len(lengths)))
@@ -117,10 +117,10 @@ def test_mixed_batch_end_to_end():
     check(out, exp)
 
 
-def run_segments(lengths, starts, heads, kvh, dim, dtype, seed, window=0, scale=None, nan_fill=True):
-    case, q, slots = build(lengths, starts, heads, kvh, dim, dtype, seed=seed, nan_fill=nan_fill)
+def run_segments(lengths, starts, heads, kvh, dim, dtype, seed, window=0, scale=None, nan_fill=True, page=16):
+    case, q, slots = build(lengths, starts, heads, kvh, dim, dtype, seed=seed, nan_fill=nan_fill, page=page)
     table = case['page_table'].to(DEV)
-    packed = packing.pack_batch(lengths, starts, slots, table)
+    packed = packing.pack_batch(lengths, starts, slots, table, page_size=page)
     out = ragged.prefill_attention(q.to(DEV), case['cache_k'].to(DEV), case['cache_v'].to(DEV), packed, table,
                                    window=window, scale=scale)
     exp = O.prefill_attention(q, case['cache_k'], case['cache_v'], lengths, starts, slots, case['page_table'],
@@ -131,9 +131,24 @@ def run_segments(lengths, starts, heads, kvh, dim, dtype, seed, window=0, scale=
 @pytest.mark.parametrize('dim', [64, 96, 128])
 @pytest.mark.parametrize('window', [0, 45])
 def test_prefill_fp32_pages(dim, window):
-    """fp32 compute dtype (qwen2.py:403-409): the vector-ALU kernel, fp32 bound."""
+    """fp32 compute dtype (qwen2.py:403-409): the fp32 MFMA kernel at D 64 / 128 and
+    the vector-ALU kernel at D 96, fp32 bound."""
     out, exp = run_segments([1, 30, 70, 129], [0, 7, 300, 20], 8, 2, dim, torch.float32, seed=dim + window,
                             window=window)
+    check(out, exp, atol=2e-5)
+
+
+@pytest.mark.parametrize('dim', [64, 128])
+@pytest.mark.parametrize('heads,kvh', [(4, 4), (14, 2), (32, 2), (128, 1), (130, 1)])
+@pytest.mark.parametrize('page,window,scale', [(16, 0, None), (64, 0, None), (32, 77, -0.09)])
+def test_prefill_fp32_groups_pages(dim, heads, kvh, page, window, scale):
+    """fp32 pages on the matrix-core kernel across GQA widths (128 columns of
+    (query row, head) per workgroup: 1 to 128 heads per KV head; 130 takes the
+    vector-ALU kernel), page sizes, a window and a negative scale."""
+    lengths = [1, 9, 130, 61] if heads <= 32 else [1, 9, 40]
+    starts = [0, 33, 500, 31] if heads <= 32 else [0, 33, 200]
+    out, exp = run_segments(lengths, starts, heads, kvh, dim, torch.float32, seed=heads + dim + page,
+                            window=window, scale=scale, page=page)
     check(out, exp, atol=2e-5)
 
 
