@@ -14,7 +14,7 @@ Prints ONE JSON line (the driver's contract) with:
   cpu_baseline the PyTorch CPU restatement (page gather + masked GQA SDPA,
                fp32) timed on the whole batch with every core of the
                affinity mask (a few seconds per step)
-Extra decode configurations (--config c2f32 / c3 / c3g32 / c5) are available for study;
+Extra decode configurations (--config c2f32 / c3 / c3g32 / c5 / c5f32) are available for study;
 the default line is C2.
 """
 import argparse
@@ -116,6 +116,13 @@ def build_case(name, device):
         case = workloads.quantize_pages(case, 32, kv_quant)
         return case, 'C3 ragged paged decode int8 KV, reference group-32 scales (fp16 per 32 channels): C2 shapes', \
             'int8', algorithmic_bytes(case, 2 * (D + 2 * (D // 32)))
+    if name == 'c5f32':
+        import torch
+        case = workloads.paged_decode_case([32768] * 16, 16, 2, 256, torch.float32, seed=5, device=device,
+                                           capacity=16 * 2048, outlier_frac=0.01)
+        D = case['query'].shape[-1]
+        return case, 'C5 shapes with fp32 pages: 16 x 32768, H16/KH2/D256, 1% K outliers x8', 'f32', \
+            algorithmic_bytes(case, 2 * D * 4)
     if name == 'c5':
         case = workloads.config_c5(device=device)
         D = case['query'].shape[-1]
@@ -178,7 +185,7 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=50)
     ap.add_argument('--warmup', type=int, default=5)
-    ap.add_argument('--config', default='c2', choices=['c2', 'c2f32', 'c3', 'c3g32', 'c4', 'c4f32', 'c5', 'rope', 'copy'])
+    ap.add_argument('--config', default='c2', choices=['c2', 'c2f32', 'c3', 'c3g32', 'c4', 'c4f32', 'c5', 'c5f32', 'rope', 'copy'])
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--copy-probe', action='store_true',
                     help='only run 1 GiB device-to-device copies (calibrates rocprofv3 FETCH/WRITE_SIZE)')

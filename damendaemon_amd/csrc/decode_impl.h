@@ -663,9 +663,8 @@ namespace dd_decode {
 
 // Instantiated once per dtype pair in decode_<dtype>.hip.  bf16 / f16 pages
 // and int8 pages with one scale per row or per 32 channels, at D = 64, 128,
-// 256, and fp32 pages at D = 64, 128 take the streamed kernels
-// (decode_stream.h); D = 96, fp32 at D = 256 and other int8 groupings take
-// decode_kernel.
+// 256, and fp32 pages at D = 64, 128, 256 take the streamed kernels
+// (decode_stream.h); D = 96 and other int8 groupings take decode_kernel.
 template <int KVT, int QT>
 int dispatch_d(const DecodeParams &p, int D, hipStream_t s, int phase) {
   if constexpr (DD_DECODE_STREAM && KVT == QT && (KVT == DD_BF16 || KVT == DD_F16)) {
@@ -683,6 +682,7 @@ int dispatch_d(const DecodeParams &p, int D, hipStream_t s, int phase) {
       switch (D) {
         case 64: return launch_stream<DD_F32, 64, DD_STREAM_NB_F32, DD_STREAM_NW_F32>(p, s, phase);
         case 128: return launch_stream<DD_F32, 128, DD_STREAM_NB_F32, DD_STREAM_NW_F32>(p, s, phase);
+        case 256: return launch_stream<DD_F32, 256, DD_STREAM_NB_F32_256, DD_STREAM_NW_F32_256>(p, s, phase);
         default: break;
       }
     }

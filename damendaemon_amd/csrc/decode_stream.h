@@ -8,8 +8,9 @@
 //
 // Memory path.  Each of the NW waves of a workgroup (sequence, KV head,
 // split) owns every NW-th 16-token chunk and a private ring of NB LDS
-// stages (bf16/f16 at D = 128 and fp32: 8 waves x 1 stage, measured 1 %
-// (16-bit) and 7 % (fp32) faster on 64 ragged contexts than 4 waves x 2).  A chunk's K and V rows are copied HBM -> LDS by direct-to-LDS
+// stages (bf16/f16 at D = 128 and fp32 at D = 64 / 128: 8 waves x 1 stage,
+// measured 1 % (16-bit) and 7 % (fp32) faster on 64 ragged contexts than
+// 4 waves x 2; fp32 at D = 256: 4 waves x 1 stage of 32 KiB).  A chunk's K and V rows are copied HBM -> LDS by direct-to-LDS
 // buffer loads (no VGPRs held while in flight), marked nontemporal because
 // every KV byte is read exactly once per step.  A stage is refilled as soon
 // as its chunk has been read into registers, so NB chunks per wave are in
@@ -55,6 +56,12 @@ typedef __attribute__((address_space(3))) void lds_void;
 #endif
 #ifndef DD_STREAM_NW_F32
 #define DD_STREAM_NW_F32 8
+#endif
+#ifndef DD_STREAM_NB_F32_256
+#define DD_STREAM_NB_F32_256 1
+#endif
+#ifndef DD_STREAM_NW_F32_256
+#define DD_STREAM_NW_F32_256 4
 #endif
 #ifndef DD_STREAM_I8_NB128
 #define DD_STREAM_I8_NB128 2
