@@ -550,8 +550,9 @@ extern "C" int dd_prefill_attention(const void *q, const void *k, const void *v,
   hipStream_t s = (hipStream_t)stream;
   Geometry geom;
   if (dtype == DD_F32 || !geometry(dim, &geom)) {
-    // fp32 pages: the fp32 MFMA kernel at D 64 / 128; other fp32 cases and
-    // other head sizes: the vector-ALU kernel (no plan)
+    // fp32 pages and head sizes without a 16-bit MFMA kernel: fp32 arithmetic
+    // on the matrix cores (head sizes in steps of 16); the rest: the
+    // vector-ALU kernel (no plan)
     PrefillGenericArgs a{};
     a.q = q;
     a.k = k;
@@ -573,10 +574,8 @@ extern "C" int dd_prefill_attention(const void *q, const void *k, const void *v,
     a.table_rows = table_rows;
     a.window = p.window;
     a.scale_log2 = scale * kLog2e;
-    if (dtype == DD_F32) {
-      const int rc = dd_prefill_f32(a, s);
-      if (rc != DD_EUNSUPPORTED) return rc;
-    }
+    const int rc = dd_prefill_f32(a, dtype, s);
+    if (rc != DD_EUNSUPPORTED) return rc;
     return dd_prefill_generic(a, dtype, s);
   }
   p.scale_log2 = __builtin_fabsf(scale) * kLog2e;

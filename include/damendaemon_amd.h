@@ -244,10 +244,10 @@ int dd_rope_batch(const void *qkv, int qkv_dtype, const void *cos,
  * damendaemon/paged.py:97-111: copy_pages gather + lower-right causal SDPA
  * of qwen2.py:754-770), without materialising the gathered K/V.
  *   q, out        (T, heads, dim) packed query / output rows, bf16, fp16 or
- *                 fp32 (bf16/fp16 at 64/128/256 take the MFMA kernel, fp32 at
- *                 64/128 with up to 128 query heads per KV head the fp32
- *                 MFMA kernel; other head sizes up to 256 in steps of 4 and
- *                 other fp32 cases a vector-ALU kernel)
+ *                 fp32 (bf16/fp16 at 64/128/256 take the 16-bit MFMA kernel;
+ *                 fp32, and 16-bit at other head sizes, the fp32-arithmetic
+ *                 MFMA kernel when dim is a multiple of 16 up to 256; other
+ *                 head sizes up to 256 in steps of 4 a vector-ALU kernel)
  *   k, v          (capacity, kv_heads, page_size, dim) pages holding every
  *                 segment's history including the chunk itself
  *   cu_seqlens    int64 (n+1), context_lens int64 (n) = start+len, slots int64 (n)

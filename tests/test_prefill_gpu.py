@@ -152,6 +152,15 @@ def test_prefill_fp32_groups_pages(dim, heads, kvh, page, window, scale):
     check(out, exp, atol=2e-5)
 
 
+@pytest.mark.parametrize('dim', [16, 48, 112, 160, 192, 256])
+@pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16, torch.float16])
+def test_prefill_fp32_arithmetic_head_sizes(dim, dtype):
+    """Head sizes in steps of 16 on the fp32-arithmetic matrix-core kernel (fp32 pages at
+    any of them; 16-bit pages where no 16-bit MFMA kernel exists, D 256 aside)."""
+    out, exp = run_segments([1, 45, 100], [0, 70, 260], 12, 4, dim, dtype, seed=dim + 3, window=90)
+    check(out, exp, atol=2e-5 if dtype == torch.float32 else 2e-3)
+
+
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize('dim', [96, 80])
 def test_prefill_other_head_sizes(dtype, dim):
