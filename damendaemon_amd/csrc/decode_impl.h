@@ -662,15 +662,17 @@ namespace dd_decode {
 #endif
 
 // Instantiated once per dtype pair in decode_<dtype>.hip.  bf16 / f16 pages
-// and int8 pages with one scale per row or per 32 channels, at D = 64, 128,
-// 256, and fp32 pages at D = 64, 128, 256 take the streamed kernels
-// (decode_stream.h); D = 96 and other int8 groupings take decode_kernel.
+// at D = 64, 96, 128, 256, int8 pages with one scale per row or per 32
+// channels and fp32 pages at D = 64, 128, 256 take the streamed kernels
+// (decode_stream.h); fp32 / int8 at D = 96 and other int8 groupings take
+// decode_kernel.
 template <int KVT, int QT>
 int dispatch_d(const DecodeParams &p, int D, hipStream_t s, int phase) {
   if constexpr (DD_DECODE_STREAM && KVT == QT && (KVT == DD_BF16 || KVT == DD_F16)) {
     if (p.G <= 16) {
       switch (D) {
         case 64: return launch_stream<KVT, 64, DD_STREAM_NB64, DD_STREAM_NW64>(p, s, phase);
+        case 96: return launch_stream<KVT, 96, DD_STREAM_NB96, DD_STREAM_NW96>(p, s, phase);
         case 128: return launch_stream<KVT, 128, DD_STREAM_NB128, DD_STREAM_NW128>(p, s, phase);
         case 256: return launch_stream<KVT, 256, DD_STREAM_NB256, DD_STREAM_NW256>(p, s, phase);
         default: break;

@@ -72,6 +72,12 @@ typedef __attribute__((address_space(3))) void lds_void;
 #ifndef DD_STREAM_NB128G
 #define DD_STREAM_NB128G 2
 #endif
+#ifndef DD_STREAM_NB96
+#define DD_STREAM_NB96 1
+#endif
+#ifndef DD_STREAM_NW96
+#define DD_STREAM_NW96 8
+#endif
 #ifndef DD_STREAM_NB64
 #define DD_STREAM_NB64 4
 #endif
@@ -122,7 +128,9 @@ DD_DEV constexpr int stream_swz(int r) {
 // one logical chunk, so the low four chunk bits are XORed with the row.
 template <int DT, int D>
 DD_DEV constexpr int stream_swz_of(int r) {
-  if constexpr (DT == DD_F32) {
+  if constexpr ((D & (D - 1)) != 0) {
+    return 0;  // rows padded by 16 bytes instead (see stream_kernel)
+  } else if constexpr (DT == DD_F32) {
     return r & 15;
   } else {
     return stream_swz<D>(r);
@@ -282,7 +290,15 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
 #if __HIP_DEVICE_COMPILE__
   constexpr bool F32 = DT == DD_F32;
   constexpr int ROWB = (F32 ? 4 : 2) * D;  // bytes per token row
-  constexpr int PAGEB = 16 * ROWB;   // one 16-token chunk of K (or V)
+  // LDS row stride: head sizes that are not powers of two (96) have rows of
+  // a chunk count no XOR swizzle tiles, so their rows get a 16-byte pad
+  // (stride 13 chunks: the 16-row K reads hit distinct banks); the DMA lanes
+  // that land on a pad, or past the 16 rows, read out of the resource's range
+  // and write zeros.
+  constexpr bool PADR = (D & (D - 1)) != 0;
+  constexpr int RSB = PADR ? ROWB + 16 : ROWB;
+  constexpr int SPR = RSB / 16;      // 16-byte LDS slots per row
+  constexpr int PAGEB = PADR ? (16 * RSB + 1023) / 1024 * 1024 : 16 * ROWB;  // one 16-token chunk of K (or V)
   constexpr int IPP = PAGEB / 1024;  // DMA instructions per chunk and plane
   constexpr int STAGE = 2 * PAGEB;
   constexpr int CPR = ROWB / 16;     // 16-byte chunks per row
@@ -347,13 +363,18 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
 #pragma unroll
   for (int j = 0; j < IPP; ++j) {
     const int e = 64 * j + lane;
-    const int r = e / CPR;
-    dma_off[j] = (unsigned)(r * ROWB + 16 * ((e % CPR) ^ stream_swz_of<DT, D>(r)));
+    if constexpr (PADR) {
+      const int r = e / SPR, c = e % SPR;
+      dma_off[j] = r < 16 && c < CPR ? (unsigned)(r * ROWB + 16 * c) : 0x40000000u;
+    } else {
+      const int r = e / CPR;
+      dma_off[j] = (unsigned)(r * ROWB + 16 * ((e % CPR) ^ stream_swz_of<DT, D>(r)));
+    }
   }
   unsigned k_addr[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c)
-    k_addr[c] = wbase + n16 * ROWB + 16 * ((F32 ? (D / 16) * kg + c : 4 * c + kg) ^ stream_swz_of<DT, D>(n16));
+    k_addr[c] = wbase + n16 * RSB + 16 * ((F32 ? (D / 16) * kg + c : 4 * c + kg) ^ stream_swz_of<DT, D>(n16));
   // V^T operand.  16-bit: transposing reads (lane: 4 keys of one dim per
   // tile).  fp32: O^T tile md, row m holds dim MD m + md, so that lane
   // (kg, n16) reads the MD contiguous dims MD n16 .. of key 4 kg + e
@@ -366,7 +387,7 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
       for (int q = 0; q < MD / 4; ++q) {
         const int r = 4 * kg + e;
         v_addr[e * (MD / 4) + q] =
-            wbase + PAGEB + r * ROWB + 16 * (((MD / 4) * n16 + q) ^ stream_swz_of<DT, D>(r));
+            wbase + PAGEB + r * RSB + 16 * (((MD / 4) * n16 + q) ^ stream_swz_of<DT, D>(r));
       }
   } else {
     const int a = lane & 15;
@@ -374,7 +395,7 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
     const int q = a & 3;
 #pragma unroll
     for (int md = 0; md < MD; ++md)
-      v_addr[md] = wbase + PAGEB + r * ROWB + 16 * ((2 * md + (q >> 1)) ^ stream_swz<D>(r)) + 8 * (q & 1);
+      v_addr[md] = wbase + PAGEB + r * RSB + 16 * ((2 * md + (q >> 1)) ^ stream_swz_of<DT, D>(r)) + 8 * (q & 1);
   }
 
   // This wave's chunks: first + i * NW, i < n.
