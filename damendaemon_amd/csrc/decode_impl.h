@@ -590,21 +590,15 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int D) {
   const int s0 = (int)(t_lo / p.split_tokens);
   const int s1 = t_hi > t_lo ? (int)((t_hi - 1) / p.split_tokens) : s0 - 1;
   const float *lse = p.lse + bh * p.splits;
-  float mm = -__builtin_inff();
-  for (int s = s0; s <= s1; ++s) mm = fmaxf(mm, lse[s]);
-  float sk = 0.f;
-  if (p.sinks) {
-    sk = p.sinks[h] * kLog2e;
-    mm = fmaxf(mm, sk);
-  }
-  float den = 0.f;
-  for (int s = s0; s <= s1; ++s) den += fast_exp2(lse[s] - mm);
-  if (p.sinks) den += fast_exp2(sk - mm);
-  const float inv = 1.f / den;
-  // Partials are read kBatch splits at a time with all loads in flight
-  // (a load-then-accumulate loop would expose one memory latency per split).
+  const float sk = p.sinks ? p.sinks[h] * kLog2e : -__builtin_inff();
+  // One online pass: kBatch splits' log-sum-exps and partials are loaded
+  // together (all in flight), then folded into a running max, denominator
+  // and sum, so a step of at most kBatch splits waits for one memory latency
+  // after the position.
   constexpr int kBatch = 8;
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float mm = sk;                        // running max (the sink included)
+    float den = p.sinks ? 1.f : 0.f;      // exp2(sink - mm)
     float o = 0.f;
     for (int s = s0; s <= s1; s += kBatch) {
       float v[kBatch], l[kBatch];
@@ -614,10 +608,22 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int D) {
         v[j] = ok ? p.part[(bh * p.splits + s + j) * D + d] : 0.f;
         l[j] = ok ? lse[s + j] : -__builtin_inff();
       }
+      float nm = mm;
 #pragma unroll
-      for (int j = 0; j < kBatch; ++j) o += fast_exp2(l[j] - mm) * v[j];
+      for (int j = 0; j < kBatch; ++j) nm = fmaxf(nm, l[j]);
+      const float base = nm == -__builtin_inff() ? 0.f : nm;
+      const float a = fast_exp2(mm - base);   // 0 while mm is -inf
+      den *= a;
+      o *= a;
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const float wgt = fast_exp2(l[j] - base);
+        den += wgt;
+        o += wgt * v[j];
+      }
+      mm = nm;
     }
-    store_as<QT>(p.out, bh * D + d, o * inv);
+    store_as<QT>(p.out, bh * D + d, o / den);
   }
 }
 
