@@ -287,7 +287,11 @@ int dispatch_f32(const PrefillGenericArgs &a, hipStream_t s) {
     case 112: return launch_f32<DT, 112>(a, s);
     case 128: return launch_f32<DT, 128>(a, s);
     case 160: return launch_f32<DT, 160>(a, s);
+    case 176: return launch_f32<DT, 176>(a, s);
     case 192: return launch_f32<DT, 192>(a, s);
+    case 208: return launch_f32<DT, 208>(a, s);
+    case 224: return launch_f32<DT, 224>(a, s);
+    case 240: return launch_f32<DT, 240>(a, s);
     case 256: return launch_f32<DT, 256>(a, s);
     default: return DD_EUNSUPPORTED;
   }

@@ -152,7 +152,7 @@ def test_prefill_fp32_groups_pages(dim, heads, kvh, page, window, scale):
     check(out, exp, atol=2e-5)
 
 
-@pytest.mark.parametrize('dim', [16, 48, 112, 160, 192, 256])
+@pytest.mark.parametrize('dim', [16, 48, 112, 160, 176, 192, 240, 256])
 @pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16, torch.float16])
 def test_prefill_fp32_arithmetic_head_sizes(dim, dtype):
     """Head sizes in steps of 16 on the fp32-arithmetic matrix-core kernel (fp32 pages at
