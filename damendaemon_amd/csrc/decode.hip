@@ -12,6 +12,10 @@ extern template int dd_decode::dispatch_d<DD_F32, DD_F32>(const DecodeParams &, 
 extern template int dd_decode::dispatch_d<DD_I8, DD_BF16>(const DecodeParams &, int, hipStream_t, int);
 extern template int dd_decode::dispatch_d<DD_I8, DD_F16>(const DecodeParams &, int, hipStream_t, int);
 
+#ifndef DD_DECODE_MIN_WG
+#define DD_DECODE_MIN_WG 512
+#endif
+
 extern "C" int dd_decode_splits(int max_context, int batch_kv, int *split_tokens) {
   if (max_context <= 0 || batch_kv <= 0) return -DD_EINVAL;
   // About six splits over the longest possible context, 256..2048 keys each
@@ -20,9 +24,17 @@ extern "C" int dd_decode_splits(int max_context, int batch_kv, int *split_tokens
   // Splits are dispatched split-major, so unused trailing splits cost one
   // early exit.  (Measured on 64 sequences of U[512, 8192] keys: 1408-key
   // splits beat 1024 by 2 % for bf16 pages and 5 % for int8 pages; 2048 is
-  // best for 16 x 32768.)
+  // best for 16 x 32768.  With few (sequence, KV head) pairs, e.g. 64 x 1 KV
+  // head, at least 512 workgroups: 34 us vs 41 us at 16 heads per KV head.)
   long st = dd_cdiv(dd_cdiv(max_context, 6), 64) * 64;
   st = st < 256 ? 256 : (st > 2048 ? 2048 : st);
+  // Few (sequence, KV head) pairs: more splits, so that the launch has at
+  // least DD_DECODE_MIN_WG workgroups.
+  const long want = dd_cdiv(DD_DECODE_MIN_WG, batch_kv);
+  if (dd_cdiv(max_context, st) < want) {
+    const long s2 = dd_cdiv(dd_cdiv(max_context, want), 64) * 64;
+    st = s2 < 256 ? 256 : (s2 < st ? s2 : st);
+  }
   if (split_tokens) *split_tokens = (int)st;
   return (int)dd_cdiv(max_context, st);
 }

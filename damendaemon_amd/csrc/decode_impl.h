@@ -669,13 +669,18 @@ namespace dd_decode {
 
 // Instantiated once per dtype pair in decode_<dtype>.hip.  bf16 / f16 pages
 // at D = 64, 96, 128, 256, int8 pages with one scale per row or per 32
-// channels and fp32 pages at D = 64, 128, 256 take the streamed kernels
+// channels and fp32 pages at D = 64, 128, 256 take the streamed kernels, any
+// number of query heads per KV head
 // (decode_stream.h); fp32 / int8 at D = 96 and other int8 groupings take
 // decode_kernel.
 template <int KVT, int QT>
-int dispatch_d(const DecodeParams &p, int D, hipStream_t s, int phase) {
+int dispatch_d(const DecodeParams &p0, int D, hipStream_t s, int phase) {
+  // streamed kernels: more than 16 query heads per KV head run as gsub
+  // workgroups of up to 16 heads (each reads the KV head's keys)
+  DecodeParams p = p0;
+  p.gsub = (p.G + 15) / 16;
   if constexpr (DD_DECODE_STREAM && KVT == QT && (KVT == DD_BF16 || KVT == DD_F16)) {
-    if (p.G <= 16) {
+    {
       switch (D) {
         case 64: return launch_stream<KVT, 64, DD_STREAM_NB64, DD_STREAM_NW64>(p, s, phase);
         case 96: return launch_stream<KVT, 96, DD_STREAM_NB96, DD_STREAM_NW96>(p, s, phase);
@@ -686,7 +691,7 @@ int dispatch_d(const DecodeParams &p, int D, hipStream_t s, int phase) {
     }
   }
   if constexpr (DD_DECODE_STREAM && KVT == DD_F32 && QT == DD_F32) {
-    if (p.G <= 16) {
+    {
       switch (D) {
         case 64: return launch_stream<DD_F32, 64, DD_STREAM_NB_F32, DD_STREAM_NW_F32>(p, s, phase);
         case 128: return launch_stream<DD_F32, 128, DD_STREAM_NB_F32, DD_STREAM_NW_F32>(p, s, phase);
@@ -696,7 +701,7 @@ int dispatch_d(const DecodeParams &p, int D, hipStream_t s, int phase) {
     }
   }
   if constexpr (DD_DECODE_STREAM && KVT == DD_I8 && (QT == DD_BF16 || QT == DD_F16)) {
-    if (p.G <= 16) {
+    {
       if (p.group == D) {
         switch (D) {
           case 64: return launch_stream_i8<QT, 64, 1, DD_STREAM_NB64, DD_STREAM_NW64>(p, s, phase);
@@ -715,10 +720,10 @@ int dispatch_d(const DecodeParams &p, int D, hipStream_t s, int phase) {
     }
   }
   switch (D) {
-    case 64: return dispatch_g<KVT, QT, 64>(p, s, phase);
-    case 96: return dispatch_g<KVT, QT, 96>(p, s, phase);
-    case 128: return dispatch_g<KVT, QT, 128>(p, s, phase);
-    case 256: return dispatch_g<KVT, QT, 256>(p, s, phase);
+    case 64: return dispatch_g<KVT, QT, 64>(p0, s, phase);
+    case 96: return dispatch_g<KVT, QT, 96>(p0, s, phase);
+    case 128: return dispatch_g<KVT, QT, 128>(p0, s, phase);
+    case 256: return dispatch_g<KVT, QT, 256>(p0, s, phase);
     default: return DD_EUNSUPPORTED;
   }
 }

@@ -224,13 +224,11 @@ DD_DEV void wait_vm() {
 // `s_o` must hold NW * 16 * (D + 4) floats and be free (no loads in flight).
 template <int DT, int D, int NW>
 DD_DEV void stream_epilogue(const DecodeParams &p, float (*s_ml)[2][16], float *s_o, const f32x4 (&o)[D / 16],
-                            float m_run, float lsum, int w, int lane, int b, int kh, int split) {
+                            float m_run, float lsum, int w, int lane, int b, long head0, int G, int split) {
   constexpr int MD = D / 16;
   constexpr int DP = D + 4;
   const int n16 = lane & 15;
   const int kg = lane >> 4;
-  const int G = p.G;
-  const long head0 = (long)b * p.H + (long)kh * G;
   lsum = xor32_sum(xor16_sum(lsum));
   if (lane < 16) {
     s_ml[w][0][lane] = m_run;
@@ -317,14 +315,19 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
   const int w = uniform(threadIdx.x >> 6);
   const int n16 = lane & 15;  // head column (S^T, P^T, O^T) / token row (K operand)
   const int kg = lane >> 4;
-  const int G = p.G;
 
+  // Workgroup (split, sequence, KV head, head group): with more than 16
+  // query heads per KV head, gsub workgroups of up to 16 heads each.
   const int wg = blockIdx.x;
-  const int nbkh = p.B * p.KH;
+  const int per_b = p.KH * p.gsub;
+  const int nbkh = p.B * per_b;
   const int split = wg / nbkh;
   const int bkh = wg - split * nbkh;
-  const int b = bkh / p.KH;
-  const int kh = bkh - b * p.KH;
+  const int b = bkh / per_b;
+  const int vk = bkh - b * per_b;
+  const int kh = vk / p.gsub;
+  const int gofs = 16 * (vk - kh * p.gsub);   // first head of this workgroup within the group
+  const int G = p.gsub > 1 ? min(16, p.G - gofs) : p.G;   // heads of this workgroup
 
   const long pos64 = p.pos[b];
   const int row = p.slots ? (int)p.slots[b] : 0;
@@ -338,7 +341,7 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
   if (s_lo >= s_hi) return;  // empty split: the merge never reads it
   const int pg_first = s_lo >> 4;
   const int pg_last = (s_hi - 1) >> 4;
-  const long head0 = (long)b * p.H + (long)kh * G;
+  const long head0 = (long)b * p.H + (long)kh * p.G + gofs;
   const bool col_on = n16 < G;
 
   // Q^T operand: lane (head n16, dims 8kg + 32c ..+8); fp32: dims
@@ -355,7 +358,7 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
     for (int c = 0; c < NC; ++c)
       qa[c] = col_on ? *(const u32x4 *)(qb + (head0 + n16) * D + 8 * kg + 32 * c) : u32x4{0, 0, 0, 0};
   }
-  float slope = (p.alibi && col_on) ? p.alibi[(long)kh * G + n16] * kLog2e : 0.f;
+  float slope = (p.alibi && col_on) ? p.alibi[(long)kh * p.G + gofs + n16] * kLog2e : 0.f;
 
   // Per-lane LDS byte offsets (loop invariant).
   const unsigned wbase = (unsigned)(size_t)(lds_void *)s_ring + (unsigned)(w * NB * STAGE);
@@ -507,7 +510,7 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
       for (int e = 0; e < 4; ++e) {
         const int t = t0 + 4 * kg + e;
         const long dist = pos64 - t > 0 ? pos64 - t : 0;
-        rb[e] = p.rel[((long)kh * G + (col_on ? n16 : 0)) * p.rel_buckets +
+        rb[e] = p.rel[((long)kh * p.G + gofs + (col_on ? n16 : 0)) * p.rel_buckets +
                       rel_bucket((int)dist, p.rel_buckets, p.rel_denom)] * kLog2e;
       }
     }
@@ -611,13 +614,13 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
   });
   wait_vm<0>();  // the trailing (empty) loads, before the ring is reused
 
-  stream_epilogue<DT, D, NW>(p, s_ml, (float *)s_ring, o, m_run, lsum, w, lane, b, kh, split);
+  stream_epilogue<DT, D, NW>(p, s_ml, (float *)s_ring, o, m_run, lsum, w, lane, b, head0, G, split);
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
 template <int DT, int D, int NB, int NW>
 int launch_stream(const DecodeParams &p, hipStream_t stream, int phase) {
-  const long grid = (long)p.B * p.KH * p.splits;
+  const long grid = (long)p.B * p.KH * p.gsub * p.splits;
   if (grid <= 0) return DD_OK;
   if (grid > 0x7fffffffL) return DD_EINVAL;
   if (phase & 1) {
@@ -710,14 +713,19 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
   const int w = uniform(threadIdx.x >> 6);
   const int n16 = lane & 15;
   const int kg = lane >> 4;
-  const int G = p.G;
 
+  // Workgroup (split, sequence, KV head, head group): with more than 16
+  // query heads per KV head, gsub workgroups of up to 16 heads each.
   const int wg = blockIdx.x;
-  const int nbkh = p.B * p.KH;
+  const int per_b = p.KH * p.gsub;
+  const int nbkh = p.B * per_b;
   const int split = wg / nbkh;
   const int bkh = wg - split * nbkh;
-  const int b = bkh / p.KH;
-  const int kh = bkh - b * p.KH;
+  const int b = bkh / per_b;
+  const int vk = bkh - b * per_b;
+  const int kh = vk / p.gsub;
+  const int gofs = 16 * (vk - kh * p.gsub);   // first head of this workgroup within the group
+  const int G = p.gsub > 1 ? min(16, p.G - gofs) : p.G;   // heads of this workgroup
 
   const long pos64 = p.pos[b];
   const int row = p.slots ? (int)p.slots[b] : 0;
@@ -731,7 +739,7 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
   if (s_lo >= s_hi) return;
   const int pg_first = s_lo >> 4;
   const int pg_last = (s_hi - 1) >> 4;
-  const long head0 = (long)b * p.H + (long)kh * G;
+  const long head0 = (long)b * p.H + (long)kh * p.G + gofs;
   const bool col_on = n16 < G;
 
   u32x4 qa[NC];
@@ -741,7 +749,7 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
     for (int c = 0; c < NC; ++c)
       qa[c] = col_on ? *(const u32x4 *)(qb + (head0 + n16) * D + 8 * kg + 32 * c) : u32x4{0, 0, 0, 0};
   }
-  float slope = (p.alibi && col_on) ? p.alibi[(long)kh * G + n16] * kLog2e : 0.f;
+  float slope = (p.alibi && col_on) ? p.alibi[(long)kh * p.G + gofs + n16] * kLog2e : 0.f;
 
   const unsigned wbase = (unsigned)(size_t)(lds_void *)s_ring + (unsigned)(w * NB * STAGE);
   // K operand: row n16 of chunk ch, 8-byte column 4c + kg.
@@ -956,7 +964,7 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
         for (int e = 0; e < 4; ++e) {
           const int t = t0 + 16 * ch + 4 * kg + e;
           const long dist = pos64 - t > 0 ? pos64 - t : 0;
-          rb[e] = p.rel[((long)kh * G + (col_on ? n16 : 0)) * p.rel_buckets +
+          rb[e] = p.rel[((long)kh * p.G + gofs + (col_on ? n16 : 0)) * p.rel_buckets +
                         rel_bucket((int)dist, p.rel_buckets, p.rel_denom)] * kLog2e;
         }
       }
@@ -1071,13 +1079,13 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
 #pragma unroll
   for (int md = 0; md < MD; ++md) o[md] -= psum[NG == 1 ? 0 : (16 * md) / 32];
 
-  stream_epilogue<QT, D, NW>(p, s_ml, (float *)s_ring, o, m_run, lsum, w, lane, b, kh, split);
+  stream_epilogue<QT, D, NW>(p, s_ml, (float *)s_ring, o, m_run, lsum, w, lane, b, head0, G, split);
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
 template <int QT, int D, int NG, int NB, int NW>
 int launch_stream_i8(const DecodeParams &p, hipStream_t stream, int phase) {
-  const long grid = (long)p.B * p.KH * p.splits;
+  const long grid = (long)p.B * p.KH * p.gsub * p.splits;
   if (grid <= 0) return DD_OK;
   if (grid > 0x7fffffffL) return DD_EINVAL;
   if (phase & 1) {

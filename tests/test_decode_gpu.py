@@ -251,6 +251,27 @@ def test_alibi_sinks_relative_bias_with_splits():
         check(run_case(case, **dev_kw), oracle_case(case, **kw), torch.float16)
 
 
+@pytest.mark.parametrize('kind', ['bf16', 'fp32', 'int8'])
+@pytest.mark.parametrize('heads,kvh', [(40, 2), (48, 1)])
+def test_wide_groups_per_head_terms(kind, heads, kvh):
+    """More than 16 query heads per KV head run as workgroups of up to 16 heads
+    (40/2: 16 + 4 heads per KV head): every head's ALiBi slope, sink and T5 bias
+    row must follow it into its workgroup."""
+    g = torch.Generator().manual_seed(heads)
+    base = torch.float32 if kind != 'bf16' else torch.bfloat16
+    case = paged_decode_case([5, 700, 2600, 4100], heads, kvh, 128, base, seed=heads + 1)
+    if kind == 'int8':
+        qk, ks = oracle.quantize_q8(case['cache_k'], 32)
+        qv, vs = oracle.quantize_q8(case['cache_v'], 32)
+        case.update(cache_k=qk, cache_v=qv, k_scale=ks, v_scale=vs, query=case['query'].to(torch.bfloat16))
+    alibi = -torch.rand(heads, generator=g) * 0.02
+    sinks = torch.randn(heads, generator=g)
+    rel = torch.randn(heads, 32, generator=g)
+    for kw in ({'alibi': alibi, 'sinks': sinks}, {'relative_bias': rel, 'relative_max_distance': 128, 'window': 900}):
+        dev_kw = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in kw.items()}
+        check(run_case(case, **dev_kw), oracle_case(case, **kw), torch.int8 if kind == 'int8' else base)
+
+
 @pytest.mark.parametrize('group', [32, 128])
 def test_int8_alibi_sinks_relative_bias(group):
     """The bias, sink and window terms on the int8 path (two chunks per step)."""
