@@ -46,3 +46,26 @@ def test_split_policy_covers_context():
         assert splits >= 1 and tokens.value % 64 == 0
         assert splits * tokens.value >= ctx > (splits - 1) * tokens.value
     assert lib.dd_decode_splits(0, 1, None) < 0
+
+
+def test_split_policy_sizes_and_occupancy():
+    """Split sizes are multiples of 64 in [256, 2048]; the tuned configurations keep
+    theirs (64 x 8 KV heads over 8192-key tables: 1408; 16 x 2 over 32768: 2048); and
+    a launch has about 512 workgroups or more unless the 256-key floor stops it."""
+    from damendaemon_amd import _native
+    lib = _native.library()
+
+    def policy(ctx, bkh):
+        tokens = ctypes.c_int()
+        splits = lib.dd_decode_splits(ctx, bkh, ctypes.byref(tokens))
+        return splits, tokens.value
+
+    assert policy(8192, 512) == (6, 1408)
+    assert policy(32768, 32) == (16, 2048)
+    for ctx in (300, 1000, 4096, 8192, 32768, 131072):
+        for bkh in (1, 8, 64, 100, 512, 4096):
+            splits, st = policy(ctx, bkh)
+            assert st % 64 == 0 and 256 <= st <= 2048
+            assert splits * st >= ctx > (splits - 1) * st
+            # rounding split sizes up to 64 keys may cost one split
+            assert splits * bkh >= 0.8 * 512 or st == 256, (ctx, bkh, splits, st)
