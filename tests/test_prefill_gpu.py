@@ -184,8 +184,9 @@ def test_prefill_wide_groups(heads, kvh):
 
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32])
 def test_prefill_history_past_table_cache(dtype):
-    """A history longer than the 8192 page-table entries the MFMA kernel
-    stages in LDS (131072 tokens at page 16): the rest come from the table."""
+    """A history longer than the page-table entries the MFMA kernels stage in
+    LDS (8192 at D 256, 3584 at D 64 / 128; 131072 / 57344 tokens at page 16):
+    the rest come from the table."""
     start = 8192 * 16 + 300
     lengths, starts = [50, 20], [start, 1000]
     out, exp = run_segments(lengths, starts, 4, 1, 64, dtype, seed=9, nan_fill=False)
