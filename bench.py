@@ -322,6 +322,10 @@ def bench_mixed(args, dev, dtype=torch.bfloat16):
     wall = time.perf_counter() - t0
     prefill_ms = statistics.mean(a.elapsed_time(b) for a, b, _ in events)
     decode_ms = statistics.mean(b.elapsed_time(c) for _, b, c in events)
+    # the same attention through ragged_attention: decode rows on a side stream beside the prefill
+    packed = packing.pack_batch(lengths, starts, slots, table)
+    ragged_ms = _event_mean_ms(lambda: ragged.ragged_attention(case['q'], ck, cv, packed, table), args.steps,
+                               args.warmup)
     tflops = flops / (prefill_ms * 1e-3) / 1e12
     ctx = [s + n for s, n in zip(starts, lengths)]
     decode_bytes = sum(ctx[n_chunks:]) * 8 * 128 * 2 * (4 if f32 else 2)
@@ -336,6 +340,7 @@ def bench_mixed(args, dev, dtype=torch.bfloat16):
                                ': 8 x 512-token chunks on contexts U[0,4096] + 120 decodes '
                                'ctx U[256,8192], H32/KH8/D128, page 16 (GPU pack + page write + attention)',
                    'prefill_kernel_ms': prefill_ms, 'decode_ms': decode_ms, 'prefill_flops': flops,
+                   'ragged_attention_ms': ragged_ms,
                    'decode_hbm_gbps': decode_bytes / (decode_ms * 1e-3) / 1e9},
         'roofline': {'bound': 'mfma', 'achieved': tflops, 'peak': peak, 'unit': 'TFLOP/s',
                      'frac': tflops / peak, 'traffic': None},

@@ -114,11 +114,37 @@ def ragged_attention(query, cache_k, cache_v, packed, page_table, window=0, scal
     while first_decode > 0 and lengths[first_decode - 1] == 1:
         first_decode -= 1
     t_decode = sum(lengths[:first_decode])
-    if first_decode > 0:
-        prefill_attention(q, cache_k, cache_v, packed, page_table, window, scale, out, (0, first_decode))
-    if first_decode < n:
+
+    def decode():
         rows = slice(t_decode, T)
         kernels.prepare_attention(q[rows].unsqueeze(2), cache_k, cache_v, packed.positions[rows],
                                   packed.slot_ids[rows], window=window, scale=scale, page_table=page_table,
                                   out=out[rows].unsqueeze(2)).run()
+
+    if first_decode > 0 and first_decode < n:
+        # The decode rows (HBM-bound) run on a side stream beside the prefill
+        # chunks (matrix cores): C4 526 us vs 586 us one after the other.  The
+        # two write disjoint rows of `out`; the caller's stream waits for both.
+        main = torch.cuda.current_stream(q.device)
+        side = _side_stream(q.device)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            decode()
+        prefill_attention(q, cache_k, cache_v, packed, page_table, window, scale, out, (0, first_decode))
+        main.wait_stream(side)
+    elif first_decode > 0:
+        prefill_attention(q, cache_k, cache_v, packed, page_table, window, scale, out, (0, first_decode))
+    elif first_decode < n:
+        decode()
     return out
+
+
+_SIDE_STREAMS = {}
+
+
+def _side_stream(device):
+    """One extra stream per device, default priority, for the decode half of a mixed batch."""
+    key = torch.device(device).index
+    if key not in _SIDE_STREAMS:
+        _SIDE_STREAMS[key] = torch.cuda.Stream(device=device)
+    return _SIDE_STREAMS[key]
