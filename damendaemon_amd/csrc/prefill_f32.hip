@@ -15,8 +15,8 @@
 // unrounded, accumulation is fp32; 16-bit outputs are rounded once at the
 // end.
 //
-// Layout.  A workgroup of W waves (8 up to D = 160, 4 above, as registers
-// allow) owns one (segment, KV head) and 16 W (query row, head) columns, a
+// Layout.  A workgroup of W = 8 waves (two per SIMD; at most 204 VGPRs up to
+// D = 256) owns one (segment, KV head) and 16 W (query row, head) columns, a
 // wave 16 of them with its Q in registers (lane (kg, n16): column n16, dims
 // (D/4) kg ..+D/4).  Per step the workgroup stages a 32-key tile of K and V
 // in LDS as fp32 (plain loads of the next tile are in flight while the
@@ -36,9 +36,6 @@
 
 namespace {
 
-#ifndef DD_PF32_W8_MAX
-#define DD_PF32_W8_MAX 160
-#endif
 constexpr int kKT = 32;            // keys per tile
 constexpr int kSub = kKT / 16;     // 16-key MFMA tiles per key tile
 constexpr float kNegInf = -__builtin_inff();
@@ -262,7 +259,7 @@ __global__ __launch_bounds__(64 * W) void prefill_f32_kernel(PrefillGenericArgs 
 
 template <int DT, int D>
 int launch_f32(PrefillGenericArgs a, hipStream_t s) {
-  constexpr int W = D <= DD_PF32_W8_MAX ? 8 : 4;
+  constexpr int W = 8;
   const int G = a.heads / a.kv_heads;
   if (G > 16 * W) return DD_EUNSUPPORTED;
   const int rows = 16 * W / G;

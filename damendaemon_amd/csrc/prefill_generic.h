@@ -28,6 +28,5 @@ int dd_prefill_generic(const PrefillGenericArgs &args, int dtype, hipStream_t st
 
 // fp32 arithmetic on the matrix cores (prefill_f32.hip): fp32 pages, and
 // bf16 / fp16 pages at head sizes without a 16-bit MFMA kernel; D a multiple
-// of 16 up to 256, at most 128 (D <= 160) or 64
-// query heads per KV head.  DD_EUNSUPPORTED for anything else.
+// of 16 up to 256, at most 128 query heads per KV head.  DD_EUNSUPPORTED for anything else.
 int dd_prefill_f32(const PrefillGenericArgs &args, int dtype, hipStream_t stream);
