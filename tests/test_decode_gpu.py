@@ -251,6 +251,23 @@ def test_alibi_sinks_relative_bias_with_splits():
         check(run_case(case, **dev_kw), oracle_case(case, **kw), torch.float16)
 
 
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize('window', [0, 200])
+def test_dim96_streamed_padded_rows(dtype, window):
+    """D = 96 on the streamed kernel (LDS rows padded by 16 bytes, the pad
+    lanes of the DMA reading out of range): NaN-filled unused pages, a page
+    boundary inside every split, ALiBi + sinks and T5 bias."""
+    g = torch.Generator().manual_seed(96 + window)
+    case = paged_decode_case([1, 17, 300, 1409, 2900, 6000], 12, 3, 96, dtype, seed=96, nan_fill=True)
+    heads = 12
+    for kw in ({}, {'alibi': -torch.rand(heads, generator=g) * 0.02, 'sinks': torch.randn(heads, generator=g)},
+               {'relative_bias': torch.randn(heads, 32, generator=g), 'relative_max_distance': 128}):
+        if window:
+            kw = dict(kw, window=window)
+        dev_kw = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in kw.items()}
+        check(run_case(case, **dev_kw), oracle_case(case, **kw), dtype)
+
+
 @pytest.mark.parametrize('kind', ['bf16', 'fp32', 'int8'])
 @pytest.mark.parametrize('heads,kvh', [(40, 2), (48, 1)])
 def test_wide_groups_per_head_terms(kind, heads, kvh):
