@@ -667,12 +667,11 @@ namespace dd_decode {
 #define DD_DECODE_STREAM 1
 #endif
 
-// Instantiated once per dtype pair in decode_<dtype>.hip.  bf16 / f16 pages
-// at D = 64, 96, 128, 256, int8 pages with one scale per row or per 32
-// channels and fp32 pages at D = 64, 128, 256 take the streamed kernels, any
-// number of query heads per KV head
-// (decode_stream.h); fp32 / int8 at D = 96 and other int8 groupings take
-// decode_kernel.
+// Instantiated once per dtype pair in decode_<dtype>.hip.  bf16 / f16 / fp32
+// pages at D = 64, 96, 128, 256 and int8 pages with one scale per row or per
+// 32 channels at D = 64, 128, 256 take the streamed kernels (decode_stream.h),
+// any number of query heads per KV head; int8 at D = 96 and other int8
+// groupings take decode_kernel.
 template <int KVT, int QT>
 int dispatch_d(const DecodeParams &p0, int D, hipStream_t s, int phase) {
   // streamed kernels: more than 16 query heads per KV head run as gsub
@@ -694,6 +693,7 @@ int dispatch_d(const DecodeParams &p0, int D, hipStream_t s, int phase) {
     {
       switch (D) {
         case 64: return launch_stream<DD_F32, 64, DD_STREAM_NB_F32, DD_STREAM_NW_F32>(p, s, phase);
+        case 96: return launch_stream<DD_F32, 96, DD_STREAM_NB_F32, DD_STREAM_NW_F32_96>(p, s, phase);
         case 128: return launch_stream<DD_F32, 128, DD_STREAM_NB_F32, DD_STREAM_NW_F32>(p, s, phase);
         case 256: return launch_stream<DD_F32, 256, DD_STREAM_NB_F32_256, DD_STREAM_NW_F32_256>(p, s, phase);
         default: break;

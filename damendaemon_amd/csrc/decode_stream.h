@@ -10,8 +10,9 @@
 // split) owns every NW-th 16-token chunk and a private ring of NB LDS
 // stages (bf16/f16 at D = 128 and fp32 at D = 64 / 128: 8 waves x 1 stage,
 // measured 1 % (16-bit) and 7 % (fp32) faster on 64 ragged contexts than
-// 4 waves x 2; fp32 at D = 256: 4 waves x 1 stage of 32 KiB).  A chunk's K and V rows are copied HBM -> LDS by direct-to-LDS
-// buffer loads (no VGPRs held while in flight), marked nontemporal because
+// 4 waves x 2; fp32 at D = 96 and 256: 4 waves x 1 stage).  A chunk's K
+// and V rows are copied HBM -> LDS by direct-to-LDS buffer loads (no VGPRs
+// held while in flight), marked nontemporal because
 // every KV byte is read exactly once per step.  A stage is refilled as soon
 // as its chunk has been read into registers, so NB chunks per wave are in
 // flight while one is computed.  A chunk's buffer resource covers only its
@@ -56,6 +57,9 @@ typedef __attribute__((address_space(3))) void lds_void;
 #endif
 #ifndef DD_STREAM_NW_F32
 #define DD_STREAM_NW_F32 8
+#endif
+#ifndef DD_STREAM_NW_F32_96
+#define DD_STREAM_NW_F32_96 4
 #endif
 #ifndef DD_STREAM_NB_F32_256
 #define DD_STREAM_NB_F32_256 1
@@ -240,13 +244,18 @@ DD_DEV void stream_epilogue(const DecodeParams &p, float (*s_ml)[2][16], float *
   for (int ww = 1; ww < NW; ++ww) mm = fmaxf(mm, s_ml[ww][0][n16]);
   const float fac = m_run == kNegInf ? 0.f : fast_exp2(m_run - mm);
   if (n16 < G) {
-    if constexpr (DT == DD_F32) {
+    if constexpr (DT == DD_F32 && MD % 4 == 0) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int q = 0; q < MD / 4; ++q)
           *(f32x4 *)&s_o[(w * 16 + n16) * DP + MD * (4 * kg + i) + 4 * q] =
               f32x4{o[4 * q][i], o[4 * q + 1][i], o[4 * q + 2][i], o[4 * q + 3][i]} * fac;
+    } else if constexpr (DT == DD_F32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int md = 0; md < MD; ++md) s_o[(w * 16 + n16) * DP + MD * (4 * kg + i) + md] = o[md][i] * fac;
     } else {
 #pragma unroll
       for (int md = 0; md < MD; ++md) *(f32x4 *)&s_o[(w * 16 + n16) * DP + 16 * md + 4 * kg] = o[md] * fac;
@@ -382,8 +391,17 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
   // tile).  fp32: O^T tile md, row m holds dim MD m + md, so that lane
   // (kg, n16) reads the MD contiguous dims MD n16 .. of key 4 kg + e
   // (MD / 4 reads of 16 bytes per key, address index e (MD / 4) + q).
-  unsigned v_addr[MD];
-  if constexpr (F32) {
+  constexpr bool V8 = F32 && MD % 4 != 0;   // fp32 V read 8 bytes at a time (D = 96)
+  unsigned v_addr[V8 ? 2 * MD : MD];
+  if constexpr (V8) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int q = 0; q < MD / 2; ++q) {
+        const int r = 4 * kg + e;
+        v_addr[e * (MD / 2) + q] = wbase + PAGEB + r * RSB + 4 * (MD * n16 + 2 * q);
+      }
+  } else if constexpr (F32) {
 #pragma unroll
     for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -463,26 +481,37 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
     const int t0 = (first + i * NW) * 16;
     u32x4 ka[NC];
     u32x2 va[F32 ? 1 : MD];
-    u32x4 vf[F32 ? MD : 1];
+    u32x4 vf[F32 && !V8 ? MD : 1];
+    u32x2 vh[V8 ? 2 * MD : 1];
 #pragma unroll
     for (int c = 0; c < NC; ++c) ka[c] = lds_read_b128<SOFF>(k_addr[c]);
+    if constexpr (V8) {
 #pragma unroll
-    for (int md = 0; md < MD; ++md) {
-      if constexpr (F32) {
-        vf[md] = lds_read_b128<SOFF>(v_addr[md]);
-      } else {
-        va[md] = lds_read_tr16<SOFF>(v_addr[md]);
+      for (int j = 0; j < 2 * MD; ++j) vh[j] = lds_read_b64<SOFF>(v_addr[j]);
+    } else {
+#pragma unroll
+      for (int md = 0; md < MD; ++md) {
+        if constexpr (F32) {
+          vf[md] = lds_read_b128<SOFF>(v_addr[md]);
+        } else {
+          va[md] = lds_read_tr16<SOFF>(v_addr[md]);
+        }
       }
     }
     wait_lds();
 #pragma unroll
     for (int c = 0; c < NC; ++c) after_wait(ka[c]);
+    if constexpr (V8) {
 #pragma unroll
-    for (int md = 0; md < MD; ++md) {
-      if constexpr (F32) {
-        after_wait(vf[md]);
-      } else {
-        after_wait(va[md]);
+      for (int j = 0; j < 2 * MD; ++j) after_wait(vh[j]);
+    } else {
+#pragma unroll
+      for (int md = 0; md < MD; ++md) {
+        if constexpr (F32) {
+          after_wait(vf[md]);
+        } else {
+          after_wait(va[md]);
+        }
       }
     }
     // The stage is in registers now: refill it with chunk i + NB.
@@ -544,16 +573,22 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           if (t0 + 4 * kg + e < s_lo) {
+            if constexpr (V8) {
 #pragma unroll
-            for (int q = 0; q < MD / 4; ++q) vf[e * (MD / 4) + q] = u32x4{0, 0, 0, 0};
+              for (int q = 0; q < MD / 2; ++q) vh[e * (MD / 2) + q] = u32x2{0, 0};
+            } else {
+#pragma unroll
+              for (int q = 0; q < MD / 4; ++q) vf[e * (MD / 4) + q] = u32x4{0, 0, 0, 0};
+            }
           }
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e)
 #pragma unroll
         for (int md = 0; md < MD; ++md)
-          o[md] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(vf[e * (MD / 4) + md / 4][md % 4]), pr[e],
-                                                       o[md], 0, 0, 0);
+          o[md] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+              __uint_as_float(V8 ? vh[e * (MD / 2) + md / 2][md % 2] : vf[V8 ? 0 : e * (MD / 4) + md / 4][md % 4]),
+              pr[e], o[md], 0, 0, 0);
     } else {
       // P^T in two 16-bit parts (high, and the residual): the P.V product
       // then carries the fp32 probabilities to ~2^-17, as the reference's fp32
