@@ -224,3 +224,38 @@ def rope_batch(qkv, cos, sin, positions, slots, cache_k, cache_v, heads, q_norm=
          ptr(query), ptr(cache_k), ptr(cache_v), DTYPE_CODES[cache_k.dtype], cache_k.shape[0], context,
          ptr(key), ptr(value), _native.stream_of(qkv))
     return (query, key, value) if materialize else query
+
+
+# The functions of this module that replace the reference's kernels-module
+# entry points one for one (damendaemon/kernels.py:213 attention, :325
+# rope_batch).  The executor's kernels module also supplies rms, swiglu,
+# rope_store and linear_fp32 (damendaemon/kernels.py:29,48,121,356; called at
+# qwen2.py:606,678,684 and paged.py:114); those are not attention and stay
+# the module's own.
+HOT_PATH = ('attention', 'rope_batch')
+
+
+def install(module):
+    """Point ``module.attention`` and ``module.rope_batch`` at this package.
+
+    ``module`` is the kernels module an executor already holds
+    (``self.kernels``, damendaemon/qwen2.py:458-461).  Only the two hot-path
+    attributes are replaced; every other attribute (rms, swiglu, rope_store,
+    linear_fp32, ...) is left as it was.  Returns ``module``.
+    """
+    missing = [name for name in HOT_PATH if not hasattr(module, name)]
+    if missing:
+        raise ValueError(f'{module!r} has no {", ".join(missing)}: not a kernels module')
+    for name in HOT_PATH:
+        setattr(module, name, globals()[name])
+    return module
+
+
+def overlay(module):
+    """A new module object with every attribute of ``module``, except that
+    ``attention`` and ``rope_batch`` come from this package; ``module`` itself
+    is not changed (for one executor: ``self.kernels = overlay(self.kernels)``)."""
+    import types
+    view = types.ModuleType(getattr(module, '__name__', 'kernels') + '+damendaemon_amd')
+    view.__dict__.update({k: v for k, v in vars(module).items() if k not in ('__name__', '__spec__', '__loader__')})
+    return install(view)
