@@ -164,22 +164,6 @@ def cpu_baseline(case, budget_s=20.0):
                       f'SDPA on {threads} threads, median of {len(times)} steps'}
 
 
-def run_probes():
-    """Build damendaemon_amd/probes/overlap.hip (hipcc, gfx950) into a temporary
-    directory and run it: exp / fma / MFMA issue rates, LDS read bandwidth and
-    the best-case prefill tile-steps, MFMA/VALU co-issue and the shader
-    clock (one JSON line each)."""
-    import subprocess
-    import tempfile
-    src = os.path.join(ROOT, 'damendaemon_amd', 'probes', 'overlap.hip')
-    with tempfile.TemporaryDirectory() as tmp:
-        exe = os.path.join(tmp, 'overlap')
-        subprocess.run([os.environ.get('HIPCC', '/opt/rocm/bin/hipcc'), '-O3', '--offload-arch=gfx950',
-                        '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops', src, '-o', exe], check=True,
-                       capture_output=True)
-        subprocess.run([exe], check=True)
-
-
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -191,11 +175,7 @@ def main():
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--copy-probe', action='store_true',
                     help='only run 1 GiB device-to-device copies (calibrates rocprofv3 FETCH/WRITE_SIZE)')
-    ap.add_argument('--probe', action='store_true',
-                    help='compile and run the hardware probes of damendaemon_amd/probes/overlap.hip')
     args = ap.parse_args()
-    if args.probe:
-        return run_probes()
     if args.copy_probe:
         src = torch.randn(1 << 28, device='cuda:0')      # 1 GiB
         dst = torch.empty_like(src)
