@@ -10,13 +10,14 @@ kernels, and a missing or stale library raises instead of silently
 computing something else.
 """
 import ctypes
+import threading
 import os
 from functools import lru_cache
 from pathlib import Path
 
 import torch
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 LIBRARY = Path(__file__).resolve().parent / '_lib' / 'libdamendaemon_amd.so'
 
 F32, F16, BF16, I8 = 0, 1, 2, 3
@@ -43,7 +44,8 @@ SIGNATURES['dd_copy_pages'] = [_p, _p, _i, _i, _p, _i, _i64, _i64, _i64, _i, _i,
 SIGNATURES['dd_rope_batch'] = [_p, _i, _p, _p, _i, _i, _p, _p, _i64, _i, _i, _i, _p, _p, _i, _f, _i,
                                _p, _i, _i, _p, _p, _p, _i, _i64, _i, _p, _p, _p]
 SIGNATURES['dd_prefill_attention'] = [_p, _p, _p, _i, _p, _p, _p, _i, _i, _i, _p, _i, _i, _i, _i, _i, _i, _i64, _i,
-                                      _f, _p, _i, _p, _p]
+                                      _f, _p, _i, _p, _p, _p]
+SIGNATURES['dd_prefill_flag_count'] = [_i, _i, _i, _i, _i, _i]
 SIGNATURES['dd_prefill_plan'] = [_p, _p, _i, _i, _i, _i, _i, _p, _i]
 SIGNATURES['dd_prefill_geometry'] = [_i, ctypes.POINTER(_i), ctypes.POINTER(_i)]
 SIGNATURES['dd_prefill_indices'] = [_i64, _i, _i, _i64, _i64, _p, _p]
@@ -109,13 +111,20 @@ class _Staging:
     def __init__(self):
         self._slots = {}   # device index -> list of [pinned uint8 buffer, event or None]
         self._next = {}
+        # slot choice, the wait on the slot's last copy, the host copy into it
+        # and the enqueue of its device copy happen under one lock, so that two
+        # host threads never fill the same pinned slot at once
+        self._lock = threading.Lock()
 
     def upload(self, host, device):
         """Asynchronous copy of the contiguous CPU tensor ``host`` to ``device``
         on the current stream; returns the device tensor."""
         host = host.contiguous()
+        with self._lock:
+            return self._upload(host, torch.device(device))
+
+    def _upload(self, host, dev):
         nbytes = host.numel() * host.element_size()
-        dev = torch.device(device)
         index = dev.index if dev.index is not None else torch.cuda.current_device()
         slots = self._slots.setdefault(index, [[None, None] for _ in range(self.SLOTS)])
         k = self._next.get(index, 0)

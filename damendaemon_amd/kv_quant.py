@@ -70,8 +70,10 @@ def store_kv(cache, slots, positions, k, v):
     dense resident pair (the contract of kv_quant.py:79-107).
 
     One GPU quantisation of K and V together and one indexed write each for
-    the int8 rows and the scales; every (slot, position) pair must have a
-    single writer.
+    the int8 rows and the scales.  When (slot, position) pairs repeat, the
+    last one in (row, token) order wins, as in the reference's row-by-row
+    loop (kv_quant.py:99-106): every duplicate writes the winner's values,
+    so the result does not depend on the order the GPU applies the writes.
     """
     data, scales = cache
     if positions.ndim != 2 or positions.shape[0] != k.shape[0] or positions.shape[1] != k.shape[2]:
@@ -83,10 +85,25 @@ def store_kv(cache, slots, positions, k, v):
         raise ValueError('KV store position exceeds the cache context')
     codes, steps = quantize_kv(torch.stack((k, v)), group)        # (2, B, KH, T, ...)
     slot_of_token = torch.as_tensor(slots, device=data.device).long()[:, None].expand(positions.shape)
-    where = (slot_of_token, slice(None), positions.to(data.device).long())
+    pos = positions.to(data.device).long()
+    winner = _last_writer(slot_of_token * data.shape[3] + pos)
+    where = (slot_of_token, slice(None), pos)
     # destination rows data[:, b-slot, :, position] are (B, T, 2, KH, ...)
-    data[(slice(None),) + where] = codes.permute(1, 3, 0, 2, 4)
-    scales[(slice(None),) + where] = steps.permute(1, 3, 0, 2, 4)
+    rows = codes.permute(1, 3, 0, 2, 4)
+    row_scales = steps.permute(1, 3, 0, 2, 4)
+    data[(slice(None),) + where] = rows.reshape((-1,) + rows.shape[2:])[winner].view(rows.shape)
+    scales[(slice(None),) + where] = row_scales.reshape((-1,) + row_scales.shape[2:])[winner].view(row_scales.shape)
+
+
+def _last_writer(keys):
+    """For each element of ``keys`` (any shape, flattened in order), the flat
+    index of the last element with the same key.  Sort-based, no host sync."""
+    flat = keys.reshape(-1)
+    ordered, perm = torch.sort(flat, stable=True)
+    last = torch.searchsorted(ordered, ordered, right=True) - 1
+    winner = torch.empty_like(perm)
+    winner[perm] = perm[last]
+    return winner
 
 
 def read_kv(cache, slots, end, dtype=torch.float32):

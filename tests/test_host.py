@@ -62,3 +62,14 @@ def test_query_rows_fit_and_known_answers():
 def test_query_rows_rejects_bad_budgets(budget):
     with pytest.raises(ValueError):
         query_rows(64, 64, 16, budget)
+
+
+def test_last_writer_picks_the_final_duplicate():
+    import torch
+    from damendaemon_amd.kv_quant import _last_writer
+    keys = torch.tensor([[5, 3, 5], [7, 3, 5]])
+    assert _last_writer(keys).tolist() == [5, 4, 5, 3, 4, 5]
+    g = torch.Generator().manual_seed(1)
+    keys = torch.randint(0, 20, (300,), generator=g)
+    want = [max(j for j in range(300) if keys[j] == keys[i]) for i in range(300)]
+    assert _last_writer(keys).tolist() == want

@@ -41,3 +41,24 @@ def test_store_and_read_dense_slots():
     rk, rv = kv_quant.read_kv((data, scales), torch.tensor([2]).cuda(), 5)
     eq, es = oracle.quantize_q8(k[0].cpu(), 32)
     assert torch.equal(rk[0].cpu(), oracle.dequantize_q8(eq, es))
+
+
+def test_store_duplicate_rows_last_wins():
+    """Two rows writing the same (slot, position): the later row's values
+    stay, as in the reference's row-by-row loop (kv_quant.py:99-106)."""
+    data, scales = kv_quant.allocate_kv(2, 2, 16, 64, 'cuda')
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn(3, 2, 4, 64, generator=g).cuda()
+    v = torch.randn(3, 2, 4, 64, generator=g).cuda()
+    slots = torch.tensor([1, 0, 1]).cuda()
+    pos = torch.tensor([[0, 1, 2, 3], [0, 1, 2, 3], [2, 3, 4, 3]]).cuda()
+    kv_quant.store_kv((data, scales), slots, pos, k, v)
+    rk, rv = kv_quant.read_kv((data, scales), torch.tensor([1]).cuda(), 5)
+    # slot 1: positions 0, 1 from row 0; 2 from row 2 (token 0); 3 from row 2's
+    # last token (token 3, which also beats its own token 1); 4 from row 2
+    want_k = torch.stack([k[0, :, 0], k[0, :, 1], k[2, :, 0], k[2, :, 3], k[2, :, 2]], dim=1).cpu()
+    want_v = torch.stack([v[0, :, 0], v[0, :, 1], v[2, :, 0], v[2, :, 3], v[2, :, 2]], dim=1).cpu()
+    eq, es = oracle.quantize_q8(want_k, 32)
+    assert torch.equal(rk[0].cpu(), oracle.dequantize_q8(eq, es))
+    eq, es = oracle.quantize_q8(want_v, 32)
+    assert torch.equal(rv[0].cpu(), oracle.dequantize_q8(eq, es))
