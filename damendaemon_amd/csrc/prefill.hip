@@ -515,15 +515,16 @@ extern "C" int dd_prefill_attention(const void *q, const void *k, const void *v,
                                     int max_context,
                                     const int32_t *page_table, int table_rows, int table_width, int heads,
                                     int kv_heads, int dim, int page_size, int64_t capacity, int window, float scale,
-                                    const int32_t *plan, int plan_len, void *out, void *stream) {
+                                    const int32_t *plan, int plan_len, int32_t *flags, void *out, void *stream) {
   if (!q || !k || !v || !cu_seqlens || !context_lens || !slots || !page_table || !out || n < 0 || max_len < 0 ||
       heads <= 0 || kv_heads <= 0 || heads % kv_heads || page_size <= 0 || capacity <= 0 || table_width <= 0)
     return DD_EINVAL;
   (void)max_context;  // any history length: page-table entries past the LDS cache come from global memory
   if (plan && plan_len <= 0) return DD_EINVAL;
-  // softmax(q.k * scale): a zero or non-finite scale has no max-tracking
-  // online form here (masked keys would meet 0 * inf)
-  if (!(scale != 0.f && __builtin_isfinite(scale))) return DD_EINVAL;
+  if (!__builtin_isfinite(scale)) return DD_EINVAL;
+  const int needs_flags = dd_prefill_flag_count(n, max_len, heads, kv_heads, dim, dtype);
+  if (needs_flags < 0) return -needs_flags;
+  if (needs_flags > 0 && scale != 0.f && !flags) return DD_EINVAL;
   if (n == 0 || max_len == 0) return DD_OK;
   PrefillParams p{};
   p.q = q;
@@ -549,11 +550,13 @@ extern "C" int dd_prefill_attention(const void *q, const void *k, const void *v,
   p.window = window > 0 ? window : 0;
   hipStream_t s = (hipStream_t)stream;
   Geometry geom;
-  if (dtype == DD_F32 || !geometry(dim, &geom)) {
-    // fp32 pages and head sizes without a 16-bit MFMA kernel: fp32 arithmetic
-    // on the matrix cores (head sizes in steps of 16); the rest: the
-    // vector-ALU kernel (no plan)
-    PrefillGenericArgs a{};
+  // fp32 pages, head sizes without a 16-bit MFMA kernel and scale 0 (every
+  // logit 0: uniform weights over the allowed keys, as SDPA gives; the
+  // 16-bit kernels take |scale| as a log2 step): fp32 arithmetic on the
+  // matrix cores (head sizes in steps of 16), else the vector-ALU kernel (no
+  // plan).  The same arguments serve the exact re-run of flagged bf16 items.
+  PrefillGenericArgs a{};
+  {
     a.q = q;
     a.k = k;
     a.v = v;
@@ -574,15 +577,34 @@ extern "C" int dd_prefill_attention(const void *q, const void *k, const void *v,
     a.table_rows = table_rows;
     a.window = p.window;
     a.scale_log2 = scale * kLog2e;
-    const int rc = dd_prefill_f32(a, dtype, s);
-    if (rc != DD_EUNSUPPORTED) return rc;
-    return dd_prefill_generic(a, dtype, s);
   }
+  auto exact = [&](const PrefillGenericArgs &args) {
+    const int rc = dd_prefill_f32(args, dtype, s);
+    return rc != DD_EUNSUPPORTED ? rc : dd_prefill_generic(args, dtype, s);
+  };
+  if (dtype == DD_F32 || !geometry(dim, &geom) || scale == 0.f) return exact(a);
   p.scale_log2 = __builtin_fabsf(scale) * kLog2e;
   p.q_sign = scale < 0.f ? 0x80008000u : 0u;
-  if (dtype == DD_BF16) return dispatch<DD_BF16>(p, dim, max_len, plan_len, s);
-  if (dtype == DD_F16) return dispatch<DD_F16>(p, dim, max_len, plan_len, s);
-  return DD_EUNSUPPORTED;
+  p.flags = needs_flags > 0 ? flags : nullptr;
+  int rc = DD_EUNSUPPORTED;
+  if (dtype == DD_BF16) rc = dispatch<DD_BF16>(p, dim, max_len, plan_len, s);
+  if (dtype == DD_F16) rc = dispatch<DD_F16>(p, dim, max_len, plan_len, s);
+  if (rc != DD_OK || !p.flags) return rc;
+  // the items the bf16 kernel flagged, again in fp32 arithmetic
+  a.flags = flags;
+  a.flag_rows = kGeom128.cols / p.G;
+  a.flag_tiles = (int)dd_cdiv(max_len, a.flag_rows);
+  return exact(a);
+}
+
+extern "C" int dd_prefill_flag_count(int n, int max_len, int heads, int kv_heads, int dim, int dtype) {
+  if (n < 0 || max_len < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads) return -DD_EINVAL;
+  // only bf16 pages at the head sizes of prefill_pipe_kernel convert V to fp16
+  if (dtype != DD_BF16 || (dim != 64 && dim != 128)) return 0;
+  const int rows = kGeom128.cols / (heads / kv_heads);
+  if (rows < 1) return 0;   // more heads per KV head than one item holds: not supported at all
+  const long count = (long)n * kv_heads * dd_cdiv(max_len, rows);
+  return count > 0x7fffffffL ? -DD_EUNSUPPORTED : (int)count;
 }
 
 extern "C" int dd_prefill_geometry(int dim, int *columns, int *keys_per_tile) {

@@ -38,6 +38,7 @@ struct PrefillParams {
   int window;
   float scale_log2;     // |scale| * log2(e)
   unsigned q_sign;      // 0x80008000 when scale < 0: q enters negated (exact), so logits use |scale|
+  int32_t *flags;       // bf16 pages, D 64/128: per work item, 1 = result must be recomputed exactly
 };
 
 template <int DT>

@@ -95,6 +95,7 @@ __global__ __launch_bounds__(64 * W) void prefill_f32_kernel(PrefillGenericArgs 
   const int start = context - len;
   const long slot = p.slots[seg];
   const int rows_here = min(rows, len - r0);
+  if (!rerun_wanted(p, grp, r0, rows_here)) return;
   const int k_hi = start + r0 + rows_here;  // exclusive
   const int k_lo = p.window > 0 ? max(0, start + r0 - p.window + 1) : 0;
   const int t_first = k_lo / kKT;

@@ -22,7 +22,23 @@ struct PrefillGenericArgs {
   int table_w, table_rows;
   int window;
   float scale_log2;     // scale * log2(e), any finite sign
+  // Re-run mode (flags != NULL): a workgroup computes its rows only if one of
+  // the 16-bit kernel's work items covering them flagged its result (item
+  // group * flag_tiles + r / flag_rows for query row r of group (segment,
+  // KV head)); otherwise it exits at once.
+  const int32_t *flags;
+  int flag_rows, flag_tiles;
 };
+
+// Whether the 16-bit kernel flagged any of the work items that cover query
+// rows r0 .. r0 + rows - 1 of group grp (always true without flags).
+__device__ inline bool rerun_wanted(const PrefillGenericArgs &p, int grp, int r0, int rows) {
+  if (!p.flags) return true;
+  int any = 0;
+  const long base = (long)grp * p.flag_tiles;
+  for (int t = r0 / p.flag_rows; t <= (r0 + rows - 1) / p.flag_rows; ++t) any |= p.flags[base + t];
+  return any != 0;
+}
 
 int dd_prefill_generic(const PrefillGenericArgs &args, int dtype, hipStream_t stream);
 

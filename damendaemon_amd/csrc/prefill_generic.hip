@@ -60,6 +60,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_generic_kernel(PrefillGen
   const int len = (int)(p.cu[seg + 1] - tok0);
   const int r0 = qt * kWaves * kRows;
   if (r0 >= len) return;
+  if (!rerun_wanted(p, seg * p.kv_heads + kh, r0, min(kWaves * kRows, len - r0))) return;
   const int context = (int)p.ctx[seg];
   const int start = context - len;
   const long slot = p.slots[seg];

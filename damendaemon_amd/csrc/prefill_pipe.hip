@@ -23,9 +23,15 @@
 //
 // Precision.  The probabilities enter P.V as fp16 (11-bit significand; one
 // bf16 rounding, 2^-9 relative, is 8x coarser and puts short-context rows
-// several 1e-3 off).  bf16 V is converted to fp16 in LDS (exact for every
+// several 1e-3 off).  bf16 V is converted to fp16 in LDS: exact for every
 // bf16 value of magnitude in [2^-14, 65504]; smaller ones round to fp16
-// subnormals, larger ones overflow).  The softmax denominators are summed
+// subnormals (absolute error <= 2^-25), larger ones become infinite.  So
+// that no result depends on that, each work item checks its output at the
+// end: a column whose largest |O| is not finite or is below 2^-12 (where an
+// absolute 2^-25 could exceed 2^-13 of the row) flags the item in p.flags,
+// and the caller's next launch recomputes the flagged items in fp32
+// arithmetic (prefill_f32.hip, 16-bit values widened exactly).  N(0,1)-like
+// data never takes that path.  The softmax denominators are summed
 // (v_dot2_f32_f16, fp32 accumulate) from exactly the fp16 P that the P.V
 // product uses.
 //
@@ -177,6 +183,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
     grp = xcd + 8 * (j / p.max_tiles);
     qt = p.max_tiles - 1 - j % p.max_tiles;
   }
+  __shared__ int s_flag;   // some column of this item needs the exact re-run
   if (grp >= p.n * p.KH) return;
   const int seg = grp / p.KH;
   const int kh = grp - seg * p.KH;
@@ -484,7 +491,8 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
     }
   }
   for (int i = tid; i < e_count && i < kTabP; i += NT) s_tab[i] = table_entry(e_first + i);
-  __syncthreads();  // s_tab
+  if (tid == 0) s_flag = 0;
+  __syncthreads();  // s_tab, s_flag
   int pk = lookup(kt_first + NKS, k_chunk);
   vm_wait<VMW>();   // K and V of tiles f and f+1 have landed
   barrier();        // ... for every wave
@@ -530,6 +538,24 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
 
   // ---- normalise and store: lane holds dims 32md + 8(r/4) + 4h2 + r%4 of its column ----
   const float l = xor32_sum(l_part);
+  if constexpr (DT == DD_BF16) {
+    if (p.flags) {
+      // largest |O| of the column (as bits: infinities and NaNs compare
+      // above every finite value), relative to the denominator
+      unsigned mb = 0;
+#pragma unroll
+      for (int md = 0; md < MD; ++md) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mb = max(mb, __float_as_uint(o[md][r]) & 0x7fffffffu);
+      }
+      mb = max(mb, (unsigned)__shfl_xor((int)mb, 32));
+      const float top = __uint_as_float(mb) / l;
+      const bool redo = colok && !(top >= 0x1p-12f && top <= 3.0e38f);
+      if (__builtin_amdgcn_ballot_w64(redo) && lane == 0) s_flag = 1;
+      __syncthreads();
+      if (tid == 0) p.flags[(long)grp * p.max_tiles + qt] = s_flag;
+    }
+  }
   if (!colok) return;
   const float inv = 1.f / l;
   const long orow = ((tok0 + r0 + qr) * p.H + (long)kh * G + gh) * D;

@@ -59,18 +59,21 @@ def prefill_plan(lengths, starts, heads, kv_heads, dim, window=0):
 
 
 def prefill_attention(query, cache_k, cache_v, packed, page_table, window=0, scale=None, out=None,
-                      segments=None):
+                      segments=None, flags=None):
     """Causal attention of every packed query token over its slot's pages.
 
     query (T, H, D) or (T, H, 1, D); ``packed`` from ``pack_batch``; the
     chunk's own K/V must already be in the pages.  ``segments`` (a, b)
-    restricts the work to segments a..b-1 (their tokens only).
+    restricts the work to segments a..b-1 (their tokens only).  ``flags``
+    (optional, int32 on the device, at least ``prefill_flag_count`` entries)
+    receives the bf16 kernel's per-item re-run flags; by default the call
+    allocates them.
     """
     q = _check(query, cache_k, cache_v, page_table)
     T, H, D = q.shape
     scale = float(D ** -.5 if scale is None else scale)
-    if not math.isfinite(scale) or scale == 0.0:
-        raise ValueError('prefill attention needs a finite, non-zero scale')
+    if not math.isfinite(scale):
+        raise ValueError('prefill attention needs a finite scale')
     if out is None:
         out = torch.empty_like(q)
     else:
@@ -92,12 +95,28 @@ def prefill_attention(query, cache_k, cache_v, packed, page_table, window=0, sca
             return out
         plan_dev = _native.upload(torch.from_numpy(plan), q.device)
         plan_len = len(plan)
+    n_flags = prefill_flag_count(b - a, max_len, H, cache_k.shape[1], D, q.dtype)
+    # per-item exactness flags of the bf16 kernel (written by the kernel itself)
+    if flags is not None:
+        if flags.dtype != torch.int32 or flags.device != q.device or flags.numel() < n_flags:
+            raise ValueError(f'flags must be int32 on the query device with at least {n_flags} entries')
+    elif n_flags:
+        flags = torch.empty(n_flags, dtype=torch.int32, device=q.device)
     call('dd_prefill_attention', ptr(q), ptr(cache_k), ptr(cache_v), DTYPE_CODES[q.dtype],
          ptr(packed.cu_seqlens[a:]), ptr(packed.context_lens[a:]), ptr(packed._meta[2, a:]), b - a, max_len, max_context,
          ptr(page_table), page_table.shape[0], page_table.shape[1], H, cache_k.shape[1], D, cache_k.shape[2],
          cache_k.shape[0], int(window or 0), scale,
-         ptr(plan_dev) if plan_dev is not None else None, plan_len, ptr(out), _native.stream_of(q))
+         ptr(plan_dev) if plan_dev is not None else None, plan_len, ptr(flags), ptr(out), _native.stream_of(q))
     return out
+
+
+def prefill_flag_count(segments, max_len, heads, kv_heads, dim, dtype):
+    """Entries of the re-run flag workspace a prefill call needs (0: none)."""
+    lib = _native.library()
+    n = lib.dd_prefill_flag_count(segments, max_len, heads, kv_heads, dim, DTYPE_CODES[dtype])
+    if n < 0:
+        raise _native.NativeError(f'dd_prefill_flag_count failed: {lib.dd_error_string(-n).decode()} ({-n})')
+    return n
 
 
 def ragged_attention(query, cache_k, cache_v, packed, page_table, window=0, scale=None):

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define DD_ABI_VERSION 3
+#define DD_ABI_VERSION 4
 
 enum dd_dtype { DD_F32 = 0, DD_F16 = 1, DD_BF16 = 2, DD_I8 = 3 };
 
@@ -253,10 +253,17 @@ int dd_rope_batch(const void *qkv, int qkv_dtype, const void *cos,
  *   cu_seqlens    int64 (n+1), context_lens int64 (n) = start+len, slots int64 (n)
  *   max_len       the longest segment (sizes the grid)
  *   max_context   the longest start+len (informational; any length)
- *   scale         any finite non-zero value (0 or non-finite: DD_EINVAL)
+ *   scale         any finite value (non-finite: DD_EINVAL); 0 gives uniform
+ *                 weights over each row's allowed keys, as SDPA does
  *   plan          NULL, or the device copy of dd_prefill_plan's output for
  *                 these same lengths/starts (plan_len entries): the
  *                 workgroup order; NULL uses a fixed XCD-aware order
+ *   flags         device int32 workspace of dd_prefill_flag_count(...)
+ *                 entries (NULL allowed when that count is 0).  The bf16
+ *                 kernel at dim 64/128 multiplies V in fp16; a work item
+ *                 whose output shows V outside fp16's normal range flags
+ *                 itself there and a second launch recomputes it in fp32
+ *                 arithmetic.  Overwritten on every call; needs no clearing.
  * Row j of segment i attends keys 0 .. start_i + j (and > that - window).
  */
 int dd_prefill_attention(const void *q, const void *k, const void *v,
@@ -267,8 +274,16 @@ int dd_prefill_attention(const void *q, const void *k, const void *v,
                          int table_rows, int table_width, int heads,
                          int kv_heads, int dim, int page_size,
                          int64_t capacity, int window, float scale,
-                         const int32_t *plan, int plan_len, void *out,
-                         void *stream);
+                         const int32_t *plan, int plan_len, int32_t *flags,
+                         void *out, void *stream);
+
+/*
+ * Entries of dd_prefill_attention's flags workspace for these arguments (0
+ * when the call needs none); negative = -DD_E*.  No reference counterpart:
+ * the exactness guard of the fp16 P.V product of bf16 pages.
+ */
+int dd_prefill_flag_count(int n, int max_len, int heads, int kv_heads,
+                          int dim, int dtype);
 
 /*
  * Host-side schedule for dd_prefill_attention (no reference counterpart:

@@ -6,12 +6,13 @@ in the output dtype.  The oracle is the reference's prefill arithmetic
 the kernel accumulates in fp32, carries the probabilities into P.V at ~17
 bits, and rounds the result once to the output dtype.
 """
+import math
 import random
 
 import pytest
 import torch
 
-from _bounds import excess
+from _bounds import excess, half_ulp
 from damendaemon_amd import packing, ragged
 from damendaemon_amd.workloads import paged_decode_case
 from oracle import paged_oracle as O
@@ -131,8 +132,8 @@ def run_segments(lengths, starts, heads, kvh, dim, dtype, seed, window=0, scale=
 @pytest.mark.parametrize('dim', [64, 96, 128])
 @pytest.mark.parametrize('window', [0, 45])
 def test_prefill_fp32_pages(dim, window):
-    """fp32 compute dtype (qwen2.py:403-409): the fp32 MFMA kernel at D 64 / 128 and
-    the vector-ALU kernel at D 96, fp32 bound."""
+    """fp32 compute dtype (qwen2.py:403-409): the fp32-arithmetic MFMA kernel
+    (prefill_f32_kernel) at every head size here, fp32 bound."""
     out, exp = run_segments([1, 30, 70, 129], [0, 7, 300, 20], 8, 2, dim, torch.float32, seed=dim + window,
                             window=window)
     check(out, exp, atol=2e-5)
@@ -202,7 +203,7 @@ def test_prefill_rejects_bad_scale_and_out():
     table = case['page_table'].to(DEV)
     packed = packing.pack_batch(lengths, starts, slots, table)
     args = (q.to(DEV), case['cache_k'].to(DEV), case['cache_v'].to(DEV), packed, table)
-    for bad in (0.0, float('inf'), float('nan')):
+    for bad in (float('inf'), float('nan'), float('-inf')):
         with pytest.raises(ValueError):
             ragged.prefill_attention(*args, scale=bad)
     wrong = torch.empty(4, 64, 4, dtype=torch.bfloat16, device=DEV).transpose(1, 2)
@@ -232,3 +233,118 @@ def test_config_c4_full_batch():
         rows = slice(cu[seg], cu[seg + 1])
         exp = O.prefill_attention(q[rows], ck, cv, [lengths[seg]], [starts[seg]], [slots[seg]], tab)
         check(out[rows], exp)
+
+
+def _relative_error(out, exp, exp_abs):
+    """max |out - exp| less the bf16 output's half ulp, relative to each row's
+    largest sum p|v| (``exp_abs``: the same attention over |V|).  A weighted
+    sum with weights good to a relative e is good to e * sum p|v|; the
+    output row itself can cancel far below that."""
+    a = out.cpu().double()
+    assert torch.isfinite(a).all(), 'non-finite output'
+    row_mag = exp_abs.amax(dim=-1, keepdim=True).clamp_min(1e-300)
+    return (((a - exp).abs() - half_ulp(exp, torch.bfloat16)) / row_mag).max().item()
+
+
+def _scaled_v_case(lengths, starts, heads, kvh, dim, seed, magnitude):
+    """bf16 pages whose V is N(0,1) times ``magnitude(shape)`` per
+    (page, KV head, token) row."""
+    case, q, slots = build(lengths, starts, heads, kvh, dim, torch.bfloat16, seed=seed)
+    cv = case['cache_v'].double()
+    mag = magnitude(cv.shape[:3] + (1,))
+    case['cache_v'] = (cv * mag).to(torch.bfloat16)
+    return case, q, slots
+
+
+@pytest.mark.parametrize('dim,heads,kvh', [(128, 16, 4), (64, 8, 2), (128, 130, 1)])
+@pytest.mark.parametrize('spread', ['rows', 1e-6, 1e-5, 3e-3, 2e5, 1e6])
+def test_prefill_bf16_value_range(dim, heads, kvh, spread):
+    """bf16 V over the whole bf16 range that matters: per-row magnitudes
+    log-uniform in 1e-6 .. 1e6 within one segment ('rows'), or a whole cache
+    scaled by one factor (tiny values that fp16 holds only as subnormals, and
+    values past fp16's 65504).  The reference upcasts to fp32
+    (kernels.py:150,158,177; SDPA in fp32 accumulation), so no magnitude may
+    cost accuracy: bound 2e-3 of each row's largest sum p|v| plus the bf16
+    output's half ulp."""
+    lengths = [1, 40, 129, 300] if heads <= 16 else [1, 9, 40]
+    starts = [0, 3, 500, 70] if heads <= 16 else [0, 17, 100]
+    seed = dim + heads + (7 if spread == 'rows' else int(abs(math.log10(spread)) * 10))
+    g = torch.Generator().manual_seed(seed)
+    if spread == 'rows':
+        magnitude = lambda shape: torch.exp(torch.empty(shape, dtype=torch.float64).uniform_(
+            math.log(1e-6), math.log(1e6), generator=g))
+    else:
+        magnitude = lambda shape: torch.full(shape, float(spread), dtype=torch.float64)
+    case, q, slots = _scaled_v_case(lengths, starts, heads, kvh, dim, seed, magnitude)
+    table = case['page_table'].to(DEV)
+    packed = packing.pack_batch(lengths, starts, slots, table)
+    out = ragged.prefill_attention(q.to(DEV), case['cache_k'].to(DEV), case['cache_v'].to(DEV), packed, table)
+    exp = O.prefill_attention(q, case['cache_k'], case['cache_v'], lengths, starts, slots, case['page_table'])
+    exp_abs = O.prefill_attention(q, case['cache_k'], case['cache_v'].abs(), lengths, starts, slots,
+                                  case['page_table'])
+    err = _relative_error(out, exp, exp_abs)
+    print(f'max error {err:.3e} of the row magnitude')
+    assert err <= 2e-3, f'max error {err:.3e} of the row magnitude'
+
+
+def test_prefill_bf16_one_huge_key():
+    """One key of V beyond fp16's range in an otherwise N(0,1) segment: every
+    row that can see it and every row that cannot (same tiles) stays exact."""
+    lengths, starts = [200], [100]
+    case, q, slots = build(lengths, starts, 8, 2, 128, torch.bfloat16, seed=91, nan_fill=True)
+    table = case['page_table']
+    j = 150                      # a history key inside the chunk's first tiles
+    case['cache_v'][int(table[0, j // 16]), 1, j % 16] *= 3e5
+    packed = packing.pack_batch(lengths, starts, slots, table.to(DEV))
+    out = ragged.prefill_attention(q.to(DEV), case['cache_k'].to(DEV), case['cache_v'].to(DEV), packed,
+                                   table.to(DEV))
+    exp = O.prefill_attention(q, case['cache_k'], case['cache_v'], lengths, starts, slots, table)
+    exp_abs = O.prefill_attention(q, case['cache_k'], case['cache_v'].abs(), lengths, starts, slots, table)
+    err = _relative_error(out, exp, exp_abs)
+    assert err <= 2e-3, f'max error {err:.3e} of the row magnitude'
+
+
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize('dim', [64, 128, 256, 96])
+def test_prefill_scale_zero(dtype, dim):
+    """scale 0: every allowed key gets the same weight (SDPA's result for a
+    zero scale), windowed or not."""
+    lengths, starts = [1, 33, 90], [0, 60, 7]
+    for window in (0, 20):
+        case, q, slots = build(lengths, starts, 8, 2, dim, dtype, seed=dim + window)
+        table = case['page_table'].to(DEV)
+        packed = packing.pack_batch(lengths, starts, slots, table)
+        out = ragged.prefill_attention(q.to(DEV), case['cache_k'].to(DEV), case['cache_v'].to(DEV), packed, table,
+                                       window=window, scale=0.0)
+        exp = O.prefill_attention(q, case['cache_k'], case['cache_v'], lengths, starts, slots,
+                                  case['page_table'], window=window, scale=0.0)
+        check(out, exp, atol=2e-5 if dtype == torch.float32 else ATOL)
+
+
+def test_prefill_bf16_rerun_flags_fire_only_where_needed():
+    """The bf16 kernel flags exactly the work items whose V leaves fp16's
+    range (here: one KV head of one segment) and none on N(0,1) data."""
+    lengths, starts = [300, 70], [40, 900]
+    heads, kvh, dim = 16, 4, 128
+    case, q, slots = build(lengths, starts, heads, kvh, dim, torch.bfloat16, seed=5)
+    table = case['page_table'].to(DEV)
+    packed = packing.pack_batch(lengths, starts, slots, table)
+    n = ragged.prefill_flag_count(2, 300, heads, kvh, dim, torch.bfloat16)
+    rows = 256 // (heads // kvh)
+    tiles = -(-300 // rows)
+    assert n == 2 * kvh * tiles
+    flags = torch.full((n,), 7, dtype=torch.int32, device=DEV)
+    args = (q.to(DEV), case['cache_k'].to(DEV))
+    ragged.prefill_attention(*args, case['cache_v'].to(DEV), packed, table, flags=flags)
+    valid = [(g * tiles + t) for g in range(2 * kvh) for t in range(-(-lengths[g // kvh] // rows))]
+    assert flags.cpu()[valid].eq(0).all()
+    # segment 1, KV head 2: one history key past fp16's range
+    cv = case['cache_v'].clone()
+    cv[int(case['page_table'][1, 5]), 2, 3] = 1e6
+    out = ragged.prefill_attention(*args, cv.to(DEV), packed, table, flags=flags)
+    got = flags.cpu()
+    hot = {(1 * kvh + 2) * tiles + t for t in range(-(-lengths[1] // rows))}
+    assert all(got[i] == (1 if i in hot else 0) for i in valid), got
+    exp = O.prefill_attention(q, case['cache_k'], cv, lengths, starts, slots, case['page_table'])
+    exp_abs = O.prefill_attention(q, case['cache_k'], cv.abs(), lengths, starts, slots, case['page_table'])
+    assert _relative_error(out, exp, exp_abs) <= 2e-3
