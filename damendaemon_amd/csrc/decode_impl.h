@@ -57,7 +57,29 @@ struct DecodeParams {
   float scale_log2;
   int paged;
   int chunk_shift;  // log2(page / 16) for paged caches
+  int xcd_units;   // int8 pages: KV heads whose scale blocks share one 128-byte line (1 = no remap)
 };
+
+// Workgroup id -> logical (split, sequence, KV head) index for the int8
+// kernel.  Workgroup w runs on XCD w % 8, and each XCD has its own L2.  The
+// fp16 scale block of one (page, KV head) is page * groups * 2 bytes (32 B
+// for 16-token pages with one scale per row), so xcd_units consecutive KV
+// heads share each 128-byte line: blocks of 8 * xcd_units workgroups are
+// permuted so that those heads run on one XCD and the line is fetched
+// once, not once per XCD.  The ordering of splits is kept.
+DD_DEV int xcd_remap(const DecodeParams &p, int wg, int nbkh) {
+  const int u = p.xcd_units;
+  if (u <= 1) return wg;
+  const int split = wg / nbkh;
+  int inner = wg - split * nbkh;
+  const int blk = 8 * u;
+  if (inner < (nbkh / blk) * blk) {
+    const int base = inner / blk;
+    const int rem = inner - base * blk;
+    inner = (base * 8 + (rem & 7)) * u + (rem >> 3);
+  }
+  return split * nbkh + inner;
+}
 
 constexpr int kWaves = 4;
 #ifndef DD_DECODE_PD

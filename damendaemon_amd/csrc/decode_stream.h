@@ -751,9 +751,9 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
 
   // Workgroup (split, sequence, KV head, head group): with more than 16
   // query heads per KV head, gsub workgroups of up to 16 heads each.
-  const int wg = blockIdx.x;
   const int per_b = p.KH * p.gsub;
   const int nbkh = p.B * per_b;
+  const int wg = xcd_remap(p, blockIdx.x, nbkh);
   const int split = wg / nbkh;
   const int bkh = wg - split * nbkh;
   const int b = bkh / per_b;
@@ -1119,10 +1119,19 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
 }
 
 template <int QT, int D, int NG, int NB, int NW>
-int launch_stream_i8(const DecodeParams &p, hipStream_t stream, int phase) {
+int launch_stream_i8(const DecodeParams &p_in, hipStream_t stream, int phase) {
+  DecodeParams p = p_in;
   const long grid = (long)p.B * p.KH * p.gsub * p.splits;
   if (grid <= 0) return DD_OK;
   if (grid > 0x7fffffffL) return DD_EINVAL;
+  // KV heads per 128-byte line of scales (the line holds whole blocks of
+  // page * NG fp16 scales when that block is at most 64 bytes)
+  const int block_bytes = p.page * NG * 2;
+  p.xcd_units = 1;
+  if (p.gsub == 1 && block_bytes <= 64) {
+    const int u = 128 / block_bytes;
+    if (p.KH % u == 0) p.xcd_units = u;
+  }
   if (phase & 1) {
     hipLaunchKernelGGL((stream_i8_kernel<QT, D, NG, NB, NW>), dim3((unsigned)grid), dim3(64 * NW), 0, stream, p);
     DD_LAUNCH_CHECK();
