@@ -73,7 +73,7 @@ def source_digest(family=None):
     return h.hexdigest()[:16]
 
 
-def measured_traffic(summary):
+def measured_traffic(summary, family='decode'):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3
     PMC summary profiles/<summary>.md (FETCH_SIZE + WRITE_SIZE, calibrated
     against a plain copy), or None when there is none or it was taken on
@@ -86,7 +86,7 @@ def measured_traffic(summary):
         if ':' in line and not line.startswith(('#', '|', ' ')):
             key, _, val = line.partition(':')
             fields[key.strip()] = val.strip().strip('`')
-    if fields.get('source_digest') != source_digest('decode') or 'traffic_bytes_per_launch' not in fields:
+    if fields.get('source_digest') != source_digest(family) or 'traffic_bytes_per_launch' not in fields:
         return None
     return int(fields['traffic_bytes_per_launch'])
 
@@ -357,57 +357,93 @@ def _hbm_line(metric, unit_value, unit, ms, nbytes, steps, warmup, dtype, worklo
             'cpu_baseline': None}
 
 
+# The secondary HBM lines rotate over independent copies of their buffers so
+# that no launch finds its inputs in the 256 MB Infinity Cache (MALL) left by
+# the previous one: the sets together exceed it by far.
+ROTATE = 4
+
+
 def bench_rope(args, dev):
     """Fused RoPE + paged K/V write (kernels.rope_batch, reference kernels.py:271-340) on the
-    C4 packed batch: 4,216 tokens, H32/KH8/D128 bf16, page 16."""
+    C4 packed batch: 4,216 tokens, H32/KH8/D128 bf16, page 16.  Four independent copies of the
+    batch (qkv rows, cos/sin tables, KV pools, page tables: ~3 GB each) are used in turn."""
     from damendaemon_amd import kernels, packing, workloads
-    case = workloads.config_c4(device=dev)
-    table, ck, cv = case['page_table'], case['cache_k'], case['cache_v']
-    packed = packing.pack_batch(case['lengths'], case['starts'], case['seg_slots'], table)
-    T, H, KH, D = packed.total_tokens, 32, 8, 128
-    g = torch.Generator(device=dev).manual_seed(7)
-    qkv = torch.randn((T, (H + 2 * KH) * D), generator=g, device=dev).to(torch.bfloat16)
-    positions_max = max(s + n for s, n in zip(case['starts'], case['lengths']))
-    ang = torch.arange(positions_max, device=dev, dtype=torch.float32)[:, None] * \
-        torch.pow(10000.0, -torch.arange(0, D, 2, device=dev, dtype=torch.float32) / D)[None, :]
-    cos = torch.cat([ang.cos(), ang.cos()], 1).to(torch.bfloat16)
-    sin = torch.cat([ang.sin(), ang.sin()], 1).to(torch.bfloat16)
+    H, KH, D = 32, 8, 128
+    sets = []
+    for r in range(ROTATE):
+        case = workloads.config_c4(device=dev, seed=4 + 11 * r)
+        table, ck, cv = case['page_table'], case['cache_k'], case['cache_v']
+        packed = packing.pack_batch(case['lengths'], case['starts'], case['seg_slots'], table)
+        T = packed.total_tokens
+        g = torch.Generator(device=dev).manual_seed(7 + r)
+        qkv = torch.randn((T, (H + 2 * KH) * D), generator=g, device=dev).to(torch.bfloat16)
+        positions_max = max(s + n for s, n in zip(case['starts'], case['lengths']))
+        ang = torch.arange(positions_max, device=dev, dtype=torch.float32)[:, None] * \
+            torch.pow(10000.0, -torch.arange(0, D, 2, device=dev, dtype=torch.float32) / D)[None, :]
+        cos = torch.cat([ang.cos(), ang.cos()], 1).to(torch.bfloat16)
+        sin = torch.cat([ang.sin(), ang.sin()], 1).to(torch.bfloat16)
+        sets.append((qkv, cos, sin, packed, ck, cv, table))
+        del case
+    turn = [0]
 
     def step():
+        qkv, cos, sin, packed, ck, cv, table = sets[turn[0] % ROTATE]
+        turn[0] += 1
         kernels.rope_batch(qkv, cos, sin, packed.positions, packed.slot_ids, ck, cv, H, page_table=table)
 
     ms = _event_mean_ms(step, args.steps, args.warmup)
+    T = sets[0][3].total_tokens
     # per token: qkv row read, cos + sin rows read, Q row written, K and V rows written into the
     # pages, position + slot ids, one page-table entry
     per_token = (H + 2 * KH) * D * 2 + 2 * D * 2 + H * D * 2 + 2 * KH * D * 2 + 16 + 4
     line = _hbm_line('fused RoPE + paged K/V write: tokens/s and achieved HBM GB/s (% peak), 1 MI355X', T,
                      'tokens/s', ms, T * per_token, args.steps, args.warmup, 'bf16',
                      'C4 packed batch through rope_batch: 4,216 tokens (8 x 512 prefill + 120 decode), '
-                     'H32/KH8/D128, rotary dim 128, page 16', 'rope', {'bytes_per_token': per_token})
+                     'H32/KH8/D128, rotary dim 128, page 16; 4 independent batches used in turn', 'rope',
+                     {'bytes_per_token': per_token, 'rotated_sets': ROTATE})
+    line['roofline']['traffic'] = measured_traffic('rope_c4_pmc', 'rope')
     print(json.dumps(line), flush=True)
 
 
 def bench_copy(args, dev):
     """copy_pages gather and restore (paged_kernels.copy_pages, reference paged_kernels.py:8-47) of one
-    32,768-token slot of the C5 geometry: KH2/D256 bf16, pages scattered over the pool."""
+    32,768-token slot of the C5 geometry: KH2/D256 bf16, pages scattered over the pool.  Four
+    independent pools (84 MB each) and dense buffers (64 MB each) are used in turn."""
     from damendaemon_amd import paged_kernels
     KH, D, P, tokens = 2, 256, 16, 32768
     pages = tokens // P
     cap = pages + pages // 4
-    g = torch.Generator(device=dev).manual_seed(9)
-    cache = torch.randn((2, cap, KH, P, D), generator=g, device=dev).to(torch.bfloat16)
-    perm = torch.randperm(cap, generator=torch.Generator().manual_seed(9))[:pages]
-    table = perm.to(torch.int32).reshape(1, pages).to(dev)
-    dense = paged_kernels.copy_pages(cache, table, 0, tokens)
-    gather_ms = _event_mean_ms(lambda: paged_kernels.copy_pages(cache, table, 0, tokens), args.steps, args.warmup)
-    restore_ms = _event_mean_ms(lambda: paged_kernels.copy_pages(cache, table, 0, tokens, dense), args.steps,
-                                args.warmup)
+    sets = []
+    for r in range(ROTATE):
+        g = torch.Generator(device=dev).manual_seed(9 + r)
+        cache = torch.randn((2, cap, KH, P, D), generator=g, device=dev).to(torch.bfloat16)
+        perm = torch.randperm(cap, generator=torch.Generator().manual_seed(9 + r))[:pages]
+        table = perm.to(torch.int32).reshape(1, pages).to(dev)
+        dense = paged_kernels.copy_pages(cache, table, 0, tokens)
+        sets.append((cache, table, dense))
+    turn = [0]
+
+    def gather():
+        cache, table, _ = sets[turn[0] % ROTATE]
+        turn[0] += 1
+        paged_kernels.copy_pages(cache, table, 0, tokens)
+
+    def restore():
+        cache, table, dense = sets[turn[0] % ROTATE]
+        turn[0] += 1
+        paged_kernels.copy_pages(cache, table, 0, tokens, dense)
+
+    gather_ms = _event_mean_ms(gather, args.steps, args.warmup)
+    restore_ms = _event_mean_ms(restore, args.steps, args.warmup)
+    dense = sets[0][2]
     nbytes = 2 * dense.numel() * dense.element_size() + pages * 4   # read + write, plus page-table entries
     line = _hbm_line('copy_pages gather: tokens/s and achieved HBM GB/s (% peak), 1 MI355X', tokens, 'tokens/s',
                      gather_ms, nbytes, args.steps, args.warmup, 'bf16',
-                     'one 32,768-token slot, KH2/D256 bf16, page 16, pages scattered (C5 geometry)', 'copy',
-                     {'restore_ms': restore_ms,
+                     'one 32,768-token slot, KH2/D256 bf16, page 16, pages scattered (C5 geometry); '
+                     '4 independent pools used in turn', 'copy',
+                     {'restore_ms': restore_ms, 'rotated_sets': ROTATE,
                       'restore_hbm_gbps': nbytes / (restore_ms * 1e-3) / 1e9})
+    line['roofline']['traffic'] = measured_traffic('copy_pages_pmc', 'copy')
     print(json.dumps(line), flush=True)
 
 
