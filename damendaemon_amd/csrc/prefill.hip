@@ -489,9 +489,17 @@ constexpr Geometry kGeom64{256, 64};   // prefill_pipe_kernel: 8 waves x 32 colu
 constexpr Geometry kGeom128{256, 64};
 constexpr Geometry kGeom256{16 * 1 * DD_PREFILL_NW, 32};
 
+// Head sizes prefill_pipe_kernel takes (48 in its 64 layout, 80-112 in its
+// 128 layout).
+static bool pipe_dim(int D) { return D == 48 || D == 64 || D == 80 || D == 96 || D == 112 || D == 128; }
+
 static bool geometry(int D, Geometry *g) {
   switch (D) {
+    case 48:
     case 64: *g = kGeom64; return true;
+    case 80:
+    case 96:
+    case 112:
     case 128: *g = kGeom128; return true;
     case 256: *g = kGeom256; return true;
     default: return false;
@@ -500,9 +508,8 @@ static bool geometry(int D, Geometry *g) {
 
 template <int DT>
 int dispatch(const PrefillParams &p, int D, int max_len, int plan_len, hipStream_t s) {
+  if (pipe_dim(D)) return prefill_pipe_dispatch(p, DT, D, max_len, plan_len, s);
   switch (D) {
-    case 64:
-    case 128: return prefill_pipe_dispatch(p, DT, D, max_len, plan_len, s);
     case 256: return launch<DT, 256, 1, kGeom256.kt, DD_PREFILL_NW>(p, max_len, plan_len, s);
     default: return DD_EUNSUPPORTED;
   }
@@ -600,7 +607,7 @@ extern "C" int dd_prefill_attention(const void *q, const void *k, const void *v,
 extern "C" int dd_prefill_flag_count(int n, int max_len, int heads, int kv_heads, int dim, int dtype) {
   if (n < 0 || max_len < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads) return -DD_EINVAL;
   // only bf16 pages at the head sizes of prefill_pipe_kernel convert V to fp16
-  if (dtype != DD_BF16 || (dim != 64 && dim != 128)) return 0;
+  if (dtype != DD_BF16 || !pipe_dim(dim)) return 0;
   const int rows = kGeom128.cols / (heads / kv_heads);
   if (rows < 1) return 0;   // more heads per KV head than one item holds: not supported at all
   const long count = (long)n * kv_heads * dd_cdiv(max_len, rows);

@@ -58,9 +58,9 @@ DD_DEV f32x4 load4(const void *base, long idx) {
   }
 }
 
+// One work item: query rows qt * rows .. of group grp = (segment, KV head).
 template <int DT, int D, int W>
-__global__ __launch_bounds__(64 * W) void prefill_f32_kernel(PrefillGenericArgs p) {
-#if __HIP_DEVICE_COMPILE__
+DD_DEV void f32_item(const PrefillGenericArgs &p, char (&s_kv)[2][2][kKT * (4 * D + 16)], int grp, int qt) {
   constexpr int NT = 64 * W;
   constexpr int COLS = 16 * W;                     // (query row, head) columns per workgroup
   constexpr int RS = 4 * D + 16;                   // LDS row stride (bytes, padded)
@@ -71,7 +71,6 @@ __global__ __launch_bounds__(64 * W) void prefill_f32_kernel(PrefillGenericArgs 
   constexpr int PCS = (kKT * PPR + NT - 1) / NT;   // pieces per thread and plane
   static_assert(D % 16 == 0 && D <= 256, "head size");
 
-  __shared__ __align__(16) char s_kv[2][2][TILEB];  // [buffer][K, V]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -79,12 +78,8 @@ __global__ __launch_bounds__(64 * W) void prefill_f32_kernel(PrefillGenericArgs 
   const int n16 = lane & 15;
   const int kg = lane >> 4;
 
-  // ---- work item: later query tiles (more keys) first ----
   const int G = p.heads / p.kv_heads;
   const int rows = COLS / G;
-  const int ngrp = p.n * p.kv_heads;
-  const int qt = p.max_tiles - 1 - (int)(blockIdx.x / ngrp);
-  const int grp = (int)(blockIdx.x % ngrp);
   const int seg = grp / p.kv_heads;
   const int kh = grp - seg * p.kv_heads;
   const long tok0 = p.cu[seg];
@@ -95,7 +90,6 @@ __global__ __launch_bounds__(64 * W) void prefill_f32_kernel(PrefillGenericArgs 
   const int start = context - len;
   const long slot = p.slots[seg];
   const int rows_here = min(rows, len - r0);
-  if (!rerun_wanted(p, grp, r0, rows_here)) return;
   const int k_hi = start + r0 + rows_here;  // exclusive
   const int k_lo = p.window > 0 ? max(0, start + r0 - p.window + 1) : 0;
   const int t_first = k_lo / kKT;
@@ -255,6 +249,42 @@ __global__ __launch_bounds__(64 * W) void prefill_f32_kernel(PrefillGenericArgs 
       for (int md = 0; md < MD; ++md) store_as<DT>(p.out, d0 + md, o[md][i] * inv);
     }
   }
+}
+
+template <int DT, int D, int W>
+__global__ __launch_bounds__(64 * W) void prefill_f32_kernel(PrefillGenericArgs p) {
+#if __HIP_DEVICE_COMPILE__
+  __shared__ __align__(16) char s_kv[2][2][kKT * (4 * D + 16)];  // [buffer][K, V], rows padded by 16 bytes
+  const int G = p.heads / p.kv_heads;
+  const int rows = 16 * W / G;
+  if (!p.flags) {
+    // one work item per workgroup, later query tiles (more keys) first
+    const int ngrp = p.n * p.kv_heads;
+    f32_item<DT, D, W>(p, s_kv, (int)(blockIdx.x % ngrp), p.max_tiles - 1 - (int)(blockIdx.x / ngrp));
+    return;
+  }
+  // Re-run of the 16-bit kernel's flagged work items: workgroup b owns group
+  // b and recomputes those of its query tiles that a flagged item covers.
+  // Every flag of the group is defined (the 16-bit kernel zeroes those of
+  // tiles past the segment), so the common case -- nothing flagged -- costs
+  // one load per lane and no other memory access.
+  const int grp = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  for (int f0 = 0; f0 < p.flag_tiles; f0 += 64) {
+    const int f = f0 + lane;
+    const unsigned long long hot =
+        __builtin_amdgcn_ballot_w64(f < p.flag_tiles && p.flags[(long)grp * p.flag_tiles + f] != 0);
+    if (!hot) continue;
+    // query tiles of this kernel that overlap the flagged items f0 + bit
+    for (int qt = (f0 * p.flag_rows) / rows; qt < p.max_tiles && qt * rows < (f0 + 64) * p.flag_rows; ++qt) {
+      const int lo = qt * rows / p.flag_rows - f0, hi = ((qt + 1) * rows - 1) / p.flag_rows - f0;
+      bool any = false;
+      for (int b = lo < 0 ? 0 : lo; b <= hi && b < 64; ++b) any |= (hot >> b) & 1;
+      if (!any) continue;
+      __syncthreads();   // the previous item's LDS reads are done
+      f32_item<DT, D, W>(p, s_kv, grp, qt);
+    }
+  }
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
@@ -265,7 +295,7 @@ int launch_f32(PrefillGenericArgs a, hipStream_t s) {
   if (G > 16 * W) return DD_EUNSUPPORTED;
   const int rows = 16 * W / G;
   a.max_tiles = (int)dd_cdiv(a.max_len, rows);
-  const long grid = (long)a.max_tiles * a.n * a.kv_heads;
+  const long grid = a.flags ? (long)a.n * a.kv_heads : (long)a.max_tiles * a.n * a.kv_heads;
   if (grid == 0) return DD_OK;
   if (grid > 0x7fffffffL) return DD_EUNSUPPORTED;
   hipLaunchKernelGGL((prefill_f32_kernel<DT, D, W>), dim3((unsigned)grid), dim3(64 * W), 0, s, a);

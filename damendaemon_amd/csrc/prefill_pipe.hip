@@ -1,5 +1,6 @@
-// Chunked-prefill attention for head sizes 64 and 128 (gfx950), bf16 or
-// fp16 pages; semantics as in prefill.hip (damendaemon/paged.py:97-111 with
+// Chunked-prefill attention for head sizes 48, 64, 80, 96, 112 and 128
+// (gfx950), bf16 or fp16 pages (48 in the 64 layout, 80-112 in the 128
+// layout: the missing dims are zeros in LDS that no MFMA reads); semantics as in prefill.hip (damendaemon/paged.py:97-111 with
 // qwen2.py:754-770): query row j of segment i attends keys 0 .. start_i + j
 // of its slot (and > position - window), GQA head h reads KV head h / G,
 // softmax(q.k * scale) . v accumulated in fp32.
@@ -142,18 +143,24 @@ DD_DEV u32x4 bf16x8_to_f16x8(u32x4 x) {
   return y;
 }
 
-template <int DT, int D>
+// D is the LDS layout's head size (64 or 128); DR <= D the real one (a
+// multiple of 16 above D / 2): rows are DR elements long in memory, the
+// layout's dims DR .. D-1 are loaded as zeros and skipped by the MFMAs.
+template <int DT, int D, int DR>
 __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
-  static_assert(D == 64 || D == 128, "head sizes 64 and 128");
+  static_assert(D == 64 || D == 128, "layouts for head sizes 64 and 128");
+  static_assert(DR % 16 == 0 && DR <= D && 2 * DR > D, "real head size");
+  constexpr int NCCR = DR / 16;         // k-steps of S^T over the real dims
+  constexpr int MDR = (DR + 31) / 32;   // 32-dim blocks of O^T holding real dims
   constexpr int NW = 8;
   constexpr int NT = 64 * NW;
   constexpr int KT = 64;                // keys per tile
-  constexpr int NCC = D / 16;           // k-steps of S^T
   constexpr int MD = D / 32;            // 32-dim blocks of O^T
   constexpr int DQ = D / 32;            // 1 KiB K blocks per 16-key chunk
   constexpr int COLS = 32 * NW;
   constexpr int PLANE = KT * D * 2;     // bytes of one K or V tile
   constexpr int IPW = DQ / 2;           // K DMA instructions per wave per tile
+  static_assert(IPW == 1 || IPW == 2, "one or two 1 KiB blocks per wave and operand");
   constexpr int VJ = PLANE / (16 * NT); // 16-byte pieces per thread of a V tile
   // loads issued after V(kt+2) that may still be in flight when this wave's
   // K(kt+2) and V(kt+2) must have landed (end of step kt): the K/V loads of
@@ -222,13 +229,20 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   const int gh = col - qr * G;
   const bool colok = qr < rows_here;
   const int qpos = start + r0 + (colok ? qr : 0);
-  u32x4 qb[NCC];   // loaded in the prologue
+  u32x4 qb[NCCR];  // loaded in the prologue
 
   // ---- loads ----
   // K: wave w fills blocks w*IPW .. +IPW of a tile (chunk b / DQ, dims 32 (b % DQ)..)
   const int kb0 = w * IPW;
   const int k_chunk = kb0 / DQ;
-  const unsigned k_dma_lane = 2u * ((lane & 15) * D + 32 * (kb0 % DQ) + 8 * (lane >> 4));
+  // lanes whose 8 dims lie past the real head size load nothing (an offset
+  // past every buffer resource reads as zero)
+  // (IPW <= 2: the per-block offsets are held as two scalars)
+  auto k_off = [&](int j) {
+    const int d0 = 32 * (kb0 % DQ + j) + 8 * (lane >> 4);
+    return d0 < DR ? 2u * ((lane & 15) * DR + d0) : 0x80000000u;
+  };
+  const unsigned k_dma0 = k_off(0), k_dma1 = DR == D ? 0u : k_off(1);
   // Page of one 16-key chunk of tile kt (-1: none, or past the last tile).
   // The lookups for a step's loads are read from LDS during the previous
   // step, so that no step starts by waiting for one.
@@ -243,16 +257,20 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
     const int phys = uniform(phys_in);
     const int live = phys < 0 ? 0 : min(16, context - key0);
     const long base =
-        phys < 0 ? 0 : ((((long)phys * p.KH + kh) << p.page_shift) | (key0 & (p.page - 1))) * (long)D;
+        phys < 0 ? 0 : ((((long)phys * p.KH + kh) << p.page_shift) | (key0 & (p.page - 1))) * (long)DR;
     return __builtin_amdgcn_make_buffer_rsrc((void *)uniform_ptr((const char *)plane + 2 * base), (short)0,
-                                             uniform(live > 0 ? live * D * 2 : 0), kBufferWord3);
+                                             uniform(live > 0 ? live * DR * 2 : 0), kBufferWord3);
   };
   auto issue_k = [&](int kt, int phys) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(p.k, kt, k_chunk, phys);
     char *dst = s_k + ((kt - kt_first) % NKS) * PLANE + kb0 * 1024;
 #pragma unroll
     for (int j = 0; j < IPW; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(dst + j * 1024), 16, k_dma_lane, 64 * j, 0, 0);
+      if constexpr (DR == D)   // block j is 32 dims (64 bytes) further along the row
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(dst + j * 1024), 16, k_dma0, 64 * j, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(dst + j * 1024), 16, j == 0 ? k_dma0 : k_dma1, 0,
+                                                 0, 0);
   };
   // V: blocks (chunk, md) of 1 KiB, the same chunk as K; DMA lane m of block
   // (c, md) brings the 16 bytes V[16c + 8(m/32) + 4((m%32)/16) + ((m%32)/2)%4]
@@ -260,18 +278,23 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   // the transposing read of region (c, md, half m/32) hands lanes 2(m%32)
   // and 2(m%32)+1.  bf16 tiles are converted to fp16 in place afterwards.
   const int vb0 = w * IPW;
-  const unsigned v_dma_lane = [&] {
+  auto v_off = [&](int j) {
     const int m = lane & 31;
     const int key = 8 * (lane >> 5) + 4 * (m >> 4) + ((m >> 1) & 3);
-    const int q8 = 4 * (vb0 % MD) + 2 * ((m >> 3) & 1) + (m & 1);
-    return (unsigned)(key * D * 2 + 16 * q8);
-  }();
+    const int q8 = 4 * (vb0 % MD + j) + 2 * ((m >> 3) & 1) + (m & 1);
+    return 8 * q8 < DR ? (unsigned)(key * DR * 2 + 16 * q8) : 0x80000000u;
+  };
+  const unsigned v_dma0 = v_off(0), v_dma1 = DR == D ? 0u : v_off(1);
   auto issue_v = [&](int kt, int phys) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(p.v, kt, k_chunk, phys);
     char *dst = s_v + ((kt - kt_first) % NVS) * PLANE + vb0 * 1024;
 #pragma unroll
     for (int j = 0; j < IPW; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(dst + j * 1024), 16, v_dma_lane, 64 * j, 0, 0);
+      if constexpr (DR == D)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(dst + j * 1024), 16, v_dma0, 64 * j, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(dst + j * 1024), 16, j == 0 ? v_dma0 : v_dma1, 0,
+                                                 0, 0);
   };
   const unsigned v_base = lds_addr(s_v);
   // bf16 V tile kt -> fp16 in place (16 contiguous bytes per lane), in two
@@ -303,7 +326,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   auto compute_s = [&](int kt, f32x16 (&s)[2]) __attribute__((always_inline)) {
     const unsigned kb_addr = k_rd + (unsigned)(((kt - kt_first) % NKS) * PLANE);
     // operand i = (cc, b) = (i / 2, i % 2); R reads in flight
-    constexpr int N = 2 * NCC, R = 4;
+    constexpr int N = 2 * NCCR, R = 4;
     auto rd = [&](int i) __attribute__((always_inline)) {
       const int cc = i >> 1, b = i & 1;
       return lds_read128(kb_addr, (2 * b * DQ + cc / 2) * 1024 + 512 * (cc & 1));
@@ -319,9 +342,9 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
       if (i + R < N) kop[i % R] = rd(i + R);
     }
   };
-  f32x16 o[MD];
+  f32x16 o[MDR];
 #pragma unroll
-  for (int md = 0; md < MD; ++md) o[md] = f32x16{};
+  for (int md = 0; md < MDR; ++md) o[md] = f32x16{};
   float m_run = kNegInf;
   float l_part = 0.f;   // this lane's share of the column's denominator
 
@@ -340,7 +363,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
     m_run = mn;
     if (__builtin_amdgcn_ballot_w64(up)) {
 #pragma unroll
-      for (int md = 0; md < MD; ++md) o[md] *= alpha;
+      for (int md = 0; md < MDR; ++md) o[md] *= alpha;
       l_part *= alpha;
     }
     return mu;
@@ -388,7 +411,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   auto mfma_phase = [&](auto has_next_c, int kt, f32x16 (&s)[2], const u32x4 (&pp)[2][2], auto &&loads)
       __attribute__((always_inline)) {
     constexpr bool HN = decltype(has_next_c)::value;
-    constexpr int NS = HN ? 2 * NCC : 0, NV = 4 * MD, N = NS + NV, R = DD_PF_RING;
+    constexpr int NS = HN ? 2 * NCCR : 0, NV = 4 * MDR, N = NS + NV, R = DD_PF_RING;
     const unsigned kb_addr = k_rd + (unsigned)(((kt + 1 - kt_first) % NKS) * PLANE);
     const unsigned vb = v_rd + (unsigned)(((kt - kt_first) % NVS) * PLANE);
     // operand i < NS: one K read; else two transposing reads
@@ -399,9 +422,9 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
         const int cc = i >> 1, b = i & 1;
         kop[i % R] = lds_read128(kb_addr, (2 * b * DQ + cc / 2) * 1024 + 512 * (cc & 1));
       } else {
-        const int j = i - NS;
-        lo[i % R] = lds_read_tr(vb, 2 * j * 512);
-        hi[i % R] = lds_read_tr(vb, 2 * j * 512 + 512);
+        const int j = i - NS, blk = (j / MDR) * MD + j % MDR;   // (key block, dim block)
+        lo[i % R] = lds_read_tr(vb, 2 * blk * 512);
+        hi[i % R] = lds_read_tr(vb, 2 * blk * 512 + 512);
       }
     };
     // LDS instructions issued after operand i while it is awaited
@@ -420,7 +443,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
         lgkm_wait(kop[i % R], after(i));
         s[b] = mfma_s<DT>(kop[i % R], qb[cc], cc == 0 ? f32x16{} : s[b]);
       } else {
-        const int j = i - NS, md = j % MD, bj = j / MD;
+        const int j = i - NS, md = j % MDR, bj = j / MDR;
         lgkm_wait(lo[i % R], hi[i % R], after(i));
         const u32x4 op = {lo[i % R][0], lo[i % R][1], hi[i % R][0], hi[i % R][1]};
         o[md] = mfma_o(op, pp[bj >> 1][bj & 1], o[md]);
@@ -483,9 +506,9 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   }
   {
     const long row = (tok0 + r0 + (colok ? qr : 0)) * p.H + (long)kh * G + gh;
-    const unsigned short *qsrc = (const unsigned short *)p.q + row * D + 8 * h2;
+    const unsigned short *qsrc = (const unsigned short *)p.q + row * DR + 8 * h2;
 #pragma unroll
-    for (int cc = 0; cc < NCC; ++cc) {
+    for (int cc = 0; cc < NCCR; ++cc) {
       const u32x4 x = *(const u32x4 *)(qsrc + 16 * cc);   // row clamped into the segment
       qb[cc] = colok ? x ^ p.q_sign : u32x4{0, 0, 0, 0};
     }
@@ -544,7 +567,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
       // above every finite value), relative to the denominator
       unsigned mb = 0;
 #pragma unroll
-      for (int md = 0; md < MD; ++md) {
+      for (int md = 0; md < MDR; ++md) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) mb = max(mb, __float_as_uint(o[md][r]) & 0x7fffffffu);
       }
@@ -554,16 +577,21 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
       if (__builtin_amdgcn_ballot_w64(redo) && lane == 0) s_flag = 1;
       __syncthreads();
       if (tid == 0) p.flags[(long)grp * p.max_tiles + qt] = s_flag;
+      // the group's first item also clears the flags of the tiles past the
+      // segment, so that every flag of a group with work is defined
+      if (qt == 0)
+        for (int t = (len + rows - 1) / rows + tid; t < p.max_tiles; t += NT) p.flags[(long)grp * p.max_tiles + t] = 0;
     }
   }
   if (!colok) return;
   const float inv = 1.f / l;
-  const long orow = ((tok0 + r0 + qr) * p.H + (long)kh * G + gh) * D;
+  const long orow = ((tok0 + r0 + qr) * p.H + (long)kh * G + gh) * DR;
   unsigned short *dst = (unsigned short *)p.out;
 #pragma unroll
-  for (int md = 0; md < MD; ++md) {
+  for (int md = 0; md < MDR; ++md) {
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
+      if (DR < D && 32 * md + 8 * q4 + 4 * h2 >= DR) continue;
       const f32x16 &x = o[md];
       const u32x2 pk = {pack2<DT>(x[4 * q4 + 0] * inv, x[4 * q4 + 1] * inv),
                         pack2<DT>(x[4 * q4 + 2] * inv, x[4 * q4 + 3] * inv)};
@@ -572,7 +600,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   }
 }
 
-template <int DT, int D>
+template <int DT, int D, int DR = D>
 int launch_pipe(PrefillParams p, int max_len, int plan_len, hipStream_t s) {
   constexpr int COLS = 256;
   if (COLS / p.G < 1) return DD_EUNSUPPORTED;
@@ -580,21 +608,29 @@ int launch_pipe(PrefillParams p, int max_len, int plan_len, hipStream_t s) {
   const long grid = p.plan ? (long)plan_len : 8L * dd_cdiv((long)p.n * p.KH, 8) * p.max_tiles;
   if (grid == 0) return DD_OK;
   if (grid > 0x7fffffffL) return DD_EUNSUPPORTED;
-  hipLaunchKernelGGL((prefill_pipe_kernel<DT, D>), dim3((unsigned)grid), dim3(512), 0, s, p);
+  hipLaunchKernelGGL((prefill_pipe_kernel<DT, D, DR>), dim3((unsigned)grid), dim3(512), 0, s, p);
   DD_LAUNCH_CHECK();
   return DD_OK;
+}
+
+template <int DT>
+int pipe_dims(const PrefillParams &p, int dim, int max_len, int plan_len, hipStream_t s) {
+  switch (dim) {
+    case 48: return launch_pipe<DT, 64, 48>(p, max_len, plan_len, s);
+    case 64: return launch_pipe<DT, 64>(p, max_len, plan_len, s);
+    case 80: return launch_pipe<DT, 128, 80>(p, max_len, plan_len, s);
+    case 96: return launch_pipe<DT, 128, 96>(p, max_len, plan_len, s);
+    case 112: return launch_pipe<DT, 128, 112>(p, max_len, plan_len, s);
+    case 128: return launch_pipe<DT, 128>(p, max_len, plan_len, s);
+    default: return DD_EUNSUPPORTED;
+  }
 }
 
 }  // namespace
 
 int prefill_pipe_dispatch(const PrefillParams &p, int dtype, int dim, int max_len, int plan_len, hipStream_t s) {
-  if (dtype == DD_BF16) {
-    if (dim == 64) return launch_pipe<DD_BF16, 64>(p, max_len, plan_len, s);
-    if (dim == 128) return launch_pipe<DD_BF16, 128>(p, max_len, plan_len, s);
-  } else if (dtype == DD_F16) {
-    if (dim == 64) return launch_pipe<DD_F16, 64>(p, max_len, plan_len, s);
-    if (dim == 128) return launch_pipe<DD_F16, 128>(p, max_len, plan_len, s);
-  }
+  if (dtype == DD_BF16) return pipe_dims<DD_BF16>(p, dim, max_len, plan_len, s);
+  if (dtype == DD_F16) return pipe_dims<DD_F16>(p, dim, max_len, plan_len, s);
   return DD_EUNSUPPORTED;
 }
 

@@ -35,6 +35,13 @@ def _check(query, cache_k, cache_v, page_table):
     return query
 
 
+def _has_mfma_geometry(dim):
+    """Whether the 16-bit MFMA prefill kernels take this head size (then the
+    call carries a workgroup plan)."""
+    cols, keys = ctypes.c_int(0), ctypes.c_int(0)
+    return _native.library().dd_prefill_geometry(int(dim), ctypes.byref(cols), ctypes.byref(keys)) == 0
+
+
 def prefill_plan(lengths, starts, heads, kv_heads, dim, window=0):
     """Workgroup order of the prefill kernel for these segments (host int32).
 
@@ -69,6 +76,14 @@ def prefill_attention(query, cache_k, cache_v, packed, page_table, window=0, sca
     receives the bf16 kernel's per-item re-run flags; by default the call
     allocates them.
     """
+    return prepare_prefill(query, cache_k, cache_v, packed, page_table, window, scale, out, segments, flags).run()
+
+
+def prepare_prefill(query, cache_k, cache_v, packed, page_table, window=0, scale=None, out=None, segments=None,
+                    flags=None):
+    """Validate a prefill call, compute and upload its workgroup plan, and
+    return a ``PrefillLaunch`` whose ``run()`` only enqueues the kernels
+    (arguments and errors as ``prefill_attention``)."""
     q = _check(query, cache_k, cache_v, page_table)
     T, H, D = q.shape
     scale = float(D ** -.5 if scale is None else scale)
@@ -83,16 +98,16 @@ def prefill_attention(query, cache_k, cache_v, packed, page_table, window=0, sca
         out = out.view(q.shape)
     a, b = segments if segments is not None else (0, len(packed.lengths))
     if b <= a:
-        return out
+        return PrefillLaunch(out, None)
     max_len = max(packed.lengths[a:b])
     max_context = max(s + n for s, n in zip(packed.starts[a:b], packed.lengths[a:b]))
     plan_dev, plan_len = None, 0
-    if q.dtype != torch.float32 and D in (64, 128, 256):
+    if q.dtype != torch.float32 and scale != 0.0 and _has_mfma_geometry(D):
         # the MFMA kernel's XCD-balanced workgroup order (the fp32 / other-D
         # kernel takes none)
         plan = prefill_plan(packed.lengths[a:b], packed.starts[a:b], H, cache_k.shape[1], D, window)
         if len(plan) == 0:
-            return out
+            return PrefillLaunch(out, None)
         plan_dev = _native.upload(torch.from_numpy(plan), q.device)
         plan_len = len(plan)
     n_flags = prefill_flag_count(b - a, max_len, H, cache_k.shape[1], D, q.dtype)
@@ -102,12 +117,27 @@ def prefill_attention(query, cache_k, cache_v, packed, page_table, window=0, sca
             raise ValueError(f'flags must be int32 on the query device with at least {n_flags} entries')
     elif n_flags:
         flags = torch.empty(n_flags, dtype=torch.int32, device=q.device)
-    call('dd_prefill_attention', ptr(q), ptr(cache_k), ptr(cache_v), DTYPE_CODES[q.dtype],
-         ptr(packed.cu_seqlens[a:]), ptr(packed.context_lens[a:]), ptr(packed._meta[2, a:]), b - a, max_len, max_context,
-         ptr(page_table), page_table.shape[0], page_table.shape[1], H, cache_k.shape[1], D, cache_k.shape[2],
-         cache_k.shape[0], int(window or 0), scale,
-         ptr(plan_dev) if plan_dev is not None else None, plan_len, ptr(flags), ptr(out), _native.stream_of(q))
-    return out
+    args = (ptr(q), ptr(cache_k), ptr(cache_v), DTYPE_CODES[q.dtype],
+            ptr(packed.cu_seqlens[a:]), ptr(packed.context_lens[a:]), ptr(packed._meta[2, a:]), b - a, max_len,
+            max_context, ptr(page_table), page_table.shape[0], page_table.shape[1], H, cache_k.shape[1], D,
+            cache_k.shape[2], cache_k.shape[0], int(window or 0), scale,
+            ptr(plan_dev) if plan_dev is not None else None, plan_len, ptr(flags), ptr(out))
+    return PrefillLaunch(out, args, keep=(q, cache_k, cache_v, packed, page_table, plan_dev, flags))
+
+
+class PrefillLaunch:
+    """One validated prefill launch (plan uploaded, output and flags
+    allocated); ``run()`` enqueues it on the current stream and returns the
+    output.  Repeated runs reuse the same buffers."""
+
+    def __init__(self, out, args, keep=()):
+        self.out, self._args, self._keep = out, args, keep
+
+    def run(self):
+        if self._args is not None:
+            call('dd_prefill_attention', *self._args,
+                 ctypes.c_void_p(torch.cuda.current_stream(self.out.device).cuda_stream))
+        return self.out
 
 
 def prefill_flag_count(segments, max_len, heads, kv_heads, dim, dtype):

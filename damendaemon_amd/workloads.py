@@ -107,7 +107,7 @@ def config_c5(device='cuda', seed=5):
                              capacity=16 * 32768 // PAGE, outlier_frac=0.01)
 
 
-def config_c4(device='cuda', seed=4, dtype=torch.bfloat16, chunks=8, chunk=512, decodes=120):
+def config_c4(device='cuda', seed=4, dtype=torch.bfloat16, chunks=8, chunk=512, decodes=120, dim=128):
     """Mixed continuous batch: ``chunks`` prefill chunks of ``chunk`` tokens appended
     to contexts U[0,4096], then ``decodes`` single-token rows with contexts U[256,8192].
 
@@ -120,11 +120,11 @@ def config_c4(device='cuda', seed=4, dtype=torch.bfloat16, chunks=8, chunk=512, 
     lengths = [chunk] * chunks + [1] * decodes
     starts = chunk_starts + [c - 1 for c in decode_ctx]
     contexts = [s + n for s, n in zip(starts, lengths)]
-    case = paged_decode_case(contexts, 32, 8, 128, dtype, seed=seed, device=device)
+    case = paged_decode_case(contexts, 32, 8, dim, dtype, seed=seed, device=device)
     gd = _gen(device, seed + 100)
     T = sum(lengths)
     case.update(lengths=lengths, starts=starts, seg_slots=list(range(len(lengths))),
-                q=torch.randn((T, 32, 128), generator=gd, device=device).to(dtype),
-                k_new=torch.randn((T, 8, 128), generator=gd, device=device).to(dtype),
-                v_new=torch.randn((T, 8, 128), generator=gd, device=device).to(dtype))
+                q=torch.randn((T, 32, dim), generator=gd, device=device).to(dtype),
+                k_new=torch.randn((T, 8, dim), generator=gd, device=device).to(dtype),
+                v_new=torch.randn((T, 8, dim), generator=gd, device=device).to(dtype))
     return case

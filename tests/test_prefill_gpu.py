@@ -163,9 +163,21 @@ def test_prefill_fp32_arithmetic_head_sizes(dim, dtype):
 
 
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize('dim', [96, 80])
+@pytest.mark.parametrize('dim', [96, 80, 112, 48])
 def test_prefill_other_head_sizes(dtype, dim):
+    """Head sizes the 16-bit MFMA kernel takes inside its 64 / 128 layouts
+    (the dims past the real head size are zeros no MFMA reads)."""
     out, exp = run_segments([3, 64, 100], [0, 200, 17], 12, 4, dim, dtype, seed=dim)
+    check(out, exp)
+
+
+@pytest.mark.parametrize('dim', [96, 80])
+@pytest.mark.parametrize('page,window,heads,kvh', [(16, 0, 32, 8), (32, 70, 8, 1), (16, 300, 130, 1)])
+def test_prefill_other_head_sizes_pages_windows(dim, page, window, heads, kvh):
+    lengths = [1, 77, 200] if heads <= 32 else [1, 9, 40]
+    starts = [5, 0, 1500] if heads <= 32 else [0, 17, 100]
+    out, exp = run_segments(lengths, starts, heads, kvh, dim, torch.bfloat16, seed=dim + page + window,
+                            window=window, page=page)
     check(out, exp)
 
 
@@ -256,7 +268,7 @@ def _scaled_v_case(lengths, starts, heads, kvh, dim, seed, magnitude):
     return case, q, slots
 
 
-@pytest.mark.parametrize('dim,heads,kvh', [(128, 16, 4), (64, 8, 2), (128, 130, 1)])
+@pytest.mark.parametrize('dim,heads,kvh', [(128, 16, 4), (64, 8, 2), (128, 130, 1), (96, 16, 4)])
 @pytest.mark.parametrize('spread', ['rows', 1e-6, 1e-5, 3e-3, 2e5, 1e6])
 def test_prefill_bf16_value_range(dim, heads, kvh, spread):
     """bf16 V over the whole bf16 range that matters: per-row magnitudes

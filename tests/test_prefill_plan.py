@@ -15,8 +15,9 @@ def _geometry(dim):
     return cols.value, kt.value
 
 
-ROWS = {d: _geometry(d)[0] for d in (64, 128, 256)}   # (query row, head) columns per workgroup
-KT = {d: _geometry(d)[1] for d in (64, 128, 256)}     # keys per tile
+DIMS = (48, 64, 80, 96, 112, 128, 256)               # head sizes with a 16-bit MFMA kernel
+ROWS = {d: _geometry(d)[0] for d in DIMS}   # (query row, head) columns per workgroup
+KT = {d: _geometry(d)[1] for d in DIMS}     # keys per tile
 
 
 def _items(lengths, starts, heads, kv_heads, dim, window):
@@ -36,7 +37,7 @@ def _items(lengths, starts, heads, kv_heads, dim, window):
 @pytest.mark.parametrize('seed', range(6))
 def test_plan_covers_every_tile_once_grouped_per_xcd_longest_first(seed):
     rng = random.Random(seed)
-    dim = rng.choice([64, 128, 256])
+    dim = rng.choice(DIMS)
     kv_heads = rng.choice([1, 2, 8])
     heads = kv_heads * rng.choice([1, 4, 8])
     n = rng.randint(1, 12)
@@ -77,7 +78,7 @@ def test_plan_rejects_bad_arguments():
     with pytest.raises(Exception):
         ragged.prefill_plan([4], [0], 6, 4, 128)     # heads not a multiple of kv_heads
     with pytest.raises(Exception):
-        ragged.prefill_plan([4], [0], 8, 2, 96)      # no prefill kernel for head dim 96
+        ragged.prefill_plan([4], [0], 8, 2, 160)     # no 16-bit MFMA kernel for head dim 160
     assert len(ragged.prefill_plan([], [], 8, 2, 128)) == 0
     cols, kt = ctypes.c_int(), ctypes.c_int()
-    assert _native.library().dd_prefill_geometry(96, ctypes.byref(cols), ctypes.byref(kt)) != 0
+    assert _native.library().dd_prefill_geometry(160, ctypes.byref(cols), ctypes.byref(kt)) != 0
