@@ -35,11 +35,14 @@ DD_DEV float half_bits_to_float(unsigned short h) {
 }
 
 // fp32 -> bf16 with round-to-nearest-even (torch's Tensor.to(bfloat16)).
+// Written without a branch (NaNs keep their payload, made quiet): as a
+// select it costs a few instructions per value; with an early return the
+// compiler puts every conversion behind its own divergent branch.
 DD_DEV unsigned short float_to_bf16_bits(float f) {
-  unsigned u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (unsigned short)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (unsigned short)(u >> 16);
+  const unsigned u = __float_as_uint(f);
+  const unsigned rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const unsigned quiet = (u >> 16) | 0x40u;
+  return (unsigned short)((u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
 }
 DD_DEV unsigned short float_to_f16_bits(float f) {
   return __builtin_bit_cast(unsigned short, (_Float16)f);

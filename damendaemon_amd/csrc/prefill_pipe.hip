@@ -218,6 +218,19 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
     const int phys = (slot_ok && e < p.table_w) ? p.table[slot * p.table_w + e] : -1;
     return (phys >= 0 && phys < p.capacity) ? phys : -1;
   };
+  // The same lookup without a branch: every lane loads (through a buffer
+  // resource over the table, so that an index past it reads 0 instead of
+  // faulting) and the result is selected afterwards.  In the prologue this
+  // keeps all of the loads in flight at once; behind a divergent branch the
+  // compiler waits for each one before the next.
+  const __amdgpu_buffer_rsrc_t tab_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)p.table, (short)0, (int)min(0x7fffffffL, (long)p.table_rows * p.table_w * 4), kBufferWord3);
+  auto table_entry_nb = [&](int e, bool want) __attribute__((always_inline)) {
+    const bool ok = want && slot_ok && e < p.table_w;
+    const long idx = ok ? slot * p.table_w + e : 0;
+    const int v = __builtin_amdgcn_raw_buffer_load_b32(tab_rsrc, (int)(4 * idx), 0, 0);
+    return (ok && v >= 0 && v < p.capacity) ? v : -1;
+  };
   auto table_at = [&](int e) -> int {   // wave-uniform
     const int i = e - e_first;
     return i < kTabP ? s_tab[i] : table_entry(e);
@@ -495,14 +508,21 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   // ---- prologue: K and V of tiles f .. f+NKS-1 in flight, V(f) in fp16, P(f) ----
   f32x16 s[2];
   u32x4 pp[2][2];   // P(kt) as fp16 P^T operands
-  // The first tiles' pages come straight from the page table, so that their
-  // loads are in flight while Q and the LDS copy of the table are fetched.
+  // All the prologue's loads go out together, each without a branch (see
+  // table_entry_nb): the first tiles' page numbers, then the item's
+  // page-table entries for the LDS copy and Q; then, once the page numbers
+  // are in, the first tiles' K/V loads.  The LDS writes of the entries wait
+  // for them alone (loads complete in order), not for the tiles.
+  int first_ph[NKS];
 #pragma unroll
-  for (int i = 0; i < NKS; ++i) {
-    const int kt = kt_first + i;
-    const int ph = kt <= kt_last ? table_entry((kt * KT + 16 * k_chunk) >> p.page_shift) : -1;
-    issue_k(kt, ph);
-    issue_v(kt, ph);
+  for (int i = 0; i < NKS; ++i)
+    first_ph[i] = table_entry_nb(((kt_first + i) * KT + 16 * k_chunk) >> p.page_shift, kt_first + i <= kt_last);
+  constexpr int kTabPer = (kTabP + NT - 1) / NT;
+  int tab_v[kTabPer];
+#pragma unroll
+  for (int j = 0; j < kTabPer; ++j) {
+    const int i = tid + NT * j;
+    tab_v[j] = table_entry_nb(e_first + i, i < e_count && i < kTabP);
   }
   {
     const long row = (tok0 + r0 + (colok ? qr : 0)) * p.H + (long)kh * G + gh;
@@ -510,12 +530,28 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
 #pragma unroll
     for (int cc = 0; cc < NCCR; ++cc) {
       const u32x4 x = *(const u32x4 *)(qsrc + 16 * cc);   // row clamped into the segment
-      qb[cc] = colok ? x ^ p.q_sign : u32x4{0, 0, 0, 0};
+      // (a mask the compiler cannot see through: every lane loads, so the
+      // loads are not put behind a branch and waited for one by one)
+      unsigned m = colok ? ~0u : 0u;
+      asm volatile("" : "+v"(m));
+      qb[cc] = (x ^ p.q_sign) & m;
     }
   }
-  for (int i = tid; i < e_count && i < kTabP; i += NT) s_tab[i] = table_entry(e_first + i);
+#pragma unroll
+  for (int i = 0; i < NKS; ++i) {
+    issue_k(kt_first + i, first_ph[i]);
+    issue_v(kt_first + i, first_ph[i]);
+  }
+#pragma unroll
+  for (int j = 0; j < kTabPer; ++j) {
+    const int i = tid + NT * j;
+    if (i < e_count && i < kTabP) s_tab[i] = tab_v[j];
+  }
   if (tid == 0) s_flag = 0;
-  __syncthreads();  // s_tab, s_flag
+  // s_tab and s_flag for every wave; no wait for the tiles in flight (a
+  // __syncthreads would wait for every load)
+  lgkm_drain();
+  barrier();
   int pk = lookup(kt_first + NKS, k_chunk);
   vm_wait<VMW>();   // K and V of tiles f and f+1 have landed
   barrier();        // ... for every wave
@@ -583,19 +619,44 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
         for (int t = (len + rows - 1) / rows + tid; t < p.max_tiles; t += NT) p.flags[(long)grp * p.max_tiles + t] = 0;
     }
   }
-  if (!colok) return;
-  const float inv = 1.f / l;
-  const long orow = ((tok0 + r0 + qr) * p.H + (long)kh * G + gh) * DR;
+  // The output goes through LDS so that every store writes whole 16-byte
+  // pieces of contiguous (query row, head) rows: stored straight from the
+  // O^T registers, each 8-byte store instruction would touch 32 rows.  Each
+  // wave writes its 32 normalised columns as rows (padded by 16 bytes) into
+  // the V ring, free once every wave has finished its last P.V reads and
+  // its loads -- the zero-size trailing ones included -- have landed.
+  lgkm_drain();
+  barrier();
+  constexpr int ORS = 2 * DR + 16;      // LDS row stride of the output tile
+  static_assert(8 * 32 * ORS <= NVS * PLANE, "output tile fits the V ring");
+  char *otile = s_v + w * 32 * ORS;
+  if (colok) {
+    const float inv = 1.f / l;
+#pragma unroll
+    for (int md = 0; md < MDR; ++md) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        if (DR < D && 32 * md + 8 * q4 + 4 * h2 >= DR) continue;
+        const f32x16 &x = o[md];
+        const u32x2 pk = {pack2<DT>(x[4 * q4 + 0] * inv, x[4 * q4 + 1] * inv),
+                          pack2<DT>(x[4 * q4 + 2] * inv, x[4 * q4 + 3] * inv)};
+        *(u32x2 *)(otile + l32 * ORS + 2 * (32 * md + 8 * q4 + 4 * h2)) = pk;
+      }
+    }
+  }
+  // (the wave reads back only what it wrote: LDS operations of one wave
+  // complete in order)
+  constexpr int PR = DR / 8;            // 16-byte pieces per row
   unsigned short *dst = (unsigned short *)p.out;
 #pragma unroll
-  for (int md = 0; md < MDR; ++md) {
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      if (DR < D && 32 * md + 8 * q4 + 4 * h2 >= DR) continue;
-      const f32x16 &x = o[md];
-      const u32x2 pk = {pack2<DT>(x[4 * q4 + 0] * inv, x[4 * q4 + 1] * inv),
-                        pack2<DT>(x[4 * q4 + 2] * inv, x[4 * q4 + 3] * inv)};
-      *(u32x2 *)(dst + orow + 32 * md + 8 * q4 + 4 * h2) = pk;
+  for (int e0 = 0; e0 < 32 * PR; e0 += 64) {
+    const int e = e0 + lane;
+    const int c = e / PR, k = e - (e / PR) * PR;
+    const int cq = (w * 32 + c) / G;
+    if (e < 32 * PR && cq < rows_here) {
+      const int cg = w * 32 + c - cq * G;
+      const u32x4 x = *(const u32x4 *)(otile + c * ORS + 16 * k);
+      *(u32x4 *)(dst + ((tok0 + r0 + cq) * p.H + (long)kh * G + cg) * DR + 8 * k) = x;
     }
   }
 }
