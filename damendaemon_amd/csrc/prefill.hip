@@ -517,12 +517,14 @@ int dispatch(const PrefillParams &p, int D, int max_len, int plan_len, hipStream
 
 }  // namespace
 
-extern "C" int dd_prefill_attention(const void *q, const void *k, const void *v, int dtype, const int64_t *cu_seqlens,
-                                    const int64_t *context_lens, const int64_t *slots, int n, int max_len,
-                                    int max_context,
-                                    const int32_t *page_table, int table_rows, int table_width, int heads,
-                                    int kv_heads, int dim, int page_size, int64_t capacity, int window, float scale,
-                                    const int32_t *plan, int plan_len, int32_t *flags, void *out, void *stream) {
+// phase bit 1: the attention kernel; bit 2: the exact re-run of the items
+// the bf16 kernel flagged (nothing to do for other calls).
+static int prefill_entry(int phase, const void *q, const void *k, const void *v, int dtype,
+                         const int64_t *cu_seqlens, const int64_t *context_lens, const int64_t *slots, int n,
+                         int max_len, int max_context, const int32_t *page_table, int table_rows, int table_width,
+                         int heads, int kv_heads, int dim, int page_size, int64_t capacity, int window, float scale,
+                         const int32_t *plan, int plan_len, int32_t *flags, void *out, void *stream) {
+  if (phase < 1 || phase > 3) return DD_EINVAL;
   if (!q || !k || !v || !cu_seqlens || !context_lens || !slots || !page_table || !out || n < 0 || max_len < 0 ||
       heads <= 0 || kv_heads <= 0 || heads % kv_heads || page_size <= 0 || capacity <= 0 || table_width <= 0)
     return DD_EINVAL;
@@ -589,19 +591,45 @@ extern "C" int dd_prefill_attention(const void *q, const void *k, const void *v,
     const int rc = dd_prefill_f32(args, dtype, s);
     return rc != DD_EUNSUPPORTED ? rc : dd_prefill_generic(args, dtype, s);
   };
-  if (dtype == DD_F32 || !geometry(dim, &geom) || scale == 0.f) return exact(a);
+  if (dtype == DD_F32 || !geometry(dim, &geom) || scale == 0.f) return (phase & 1) ? exact(a) : DD_OK;
   p.scale_log2 = __builtin_fabsf(scale) * kLog2e;
   p.q_sign = scale < 0.f ? 0x80008000u : 0u;
   p.flags = needs_flags > 0 ? flags : nullptr;
-  int rc = DD_EUNSUPPORTED;
-  if (dtype == DD_BF16) rc = dispatch<DD_BF16>(p, dim, max_len, plan_len, s);
-  if (dtype == DD_F16) rc = dispatch<DD_F16>(p, dim, max_len, plan_len, s);
-  if (rc != DD_OK || !p.flags) return rc;
+  int rc = DD_OK;
+  if (phase & 1) {
+    rc = DD_EUNSUPPORTED;
+    if (dtype == DD_BF16) rc = dispatch<DD_BF16>(p, dim, max_len, plan_len, s);
+    if (dtype == DD_F16) rc = dispatch<DD_F16>(p, dim, max_len, plan_len, s);
+  }
+  if (rc != DD_OK || !p.flags || !(phase & 2)) return rc;
   // the items the bf16 kernel flagged, again in fp32 arithmetic
   a.flags = flags;
   a.flag_rows = kGeom128.cols / p.G;
   a.flag_tiles = (int)dd_cdiv(max_len, a.flag_rows);
   return exact(a);
+}
+
+extern "C" int dd_prefill_attention(const void *q, const void *k, const void *v, int dtype, const int64_t *cu_seqlens,
+                                    const int64_t *context_lens, const int64_t *slots, int n, int max_len,
+                                    int max_context, const int32_t *page_table, int table_rows, int table_width,
+                                    int heads, int kv_heads, int dim, int page_size, int64_t capacity, int window,
+                                    float scale, const int32_t *plan, int plan_len, int32_t *flags, void *out,
+                                    void *stream) {
+  return prefill_entry(3, q, k, v, dtype, cu_seqlens, context_lens, slots, n, max_len, max_context, page_table,
+                       table_rows, table_width, heads, kv_heads, dim, page_size, capacity, window, scale, plan,
+                       plan_len, flags, out, stream);
+}
+
+extern "C" int dd_prefill_attention_phase(const void *q, const void *k, const void *v, int dtype,
+                                          const int64_t *cu_seqlens, const int64_t *context_lens,
+                                          const int64_t *slots, int n, int max_len, int max_context,
+                                          const int32_t *page_table, int table_rows, int table_width, int heads,
+                                          int kv_heads, int dim, int page_size, int64_t capacity, int window,
+                                          float scale, const int32_t *plan, int plan_len, int32_t *flags, void *out,
+                                          int phase, void *stream) {
+  return prefill_entry(phase, q, k, v, dtype, cu_seqlens, context_lens, slots, n, max_len, max_context, page_table,
+                       table_rows, table_width, heads, kv_heads, dim, page_size, capacity, window, scale, plan,
+                       plan_len, flags, out, stream);
 }
 
 extern "C" int dd_prefill_flag_count(int n, int max_len, int heads, int kv_heads, int dim, int dtype) {

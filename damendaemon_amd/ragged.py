@@ -139,6 +139,14 @@ class PrefillLaunch:
                  ctypes.c_void_p(torch.cuda.current_stream(self.out.device).cuda_stream))
         return self.out
 
+    def phase(self, which):
+        """Enqueue one launch of the call: 1 the attention kernel, 2 the exact
+        re-run of the items the bf16 kernel flagged (both together = run())."""
+        if self._args is not None:
+            call('dd_prefill_attention_phase', *self._args, int(which),
+                 ctypes.c_void_p(torch.cuda.current_stream(self.out.device).cuda_stream))
+        return self.out
+
 
 def prefill_flag_count(segments, max_len, heads, kv_heads, dim, dtype):
     """Entries of the re-run flag workspace a prefill call needs (0: none)."""

@@ -283,6 +283,23 @@ int dd_prefill_attention(const void *q, const void *k, const void *v,
                          void *out, void *stream);
 
 /*
+ * dd_prefill_attention in two launches (same arguments): phase 1 runs the
+ * attention kernel, phase 2 the exact re-run of the work items the bf16
+ * kernel flagged (a no-op for calls without a flags workspace); 3 = both,
+ * as dd_prefill_attention.  For timing the attention kernel on its own.
+ */
+int dd_prefill_attention_phase(const void *q, const void *k, const void *v,
+                               int dtype, const int64_t *cu_seqlens,
+                               const int64_t *context_lens, const int64_t *slots,
+                               int n, int max_len, int max_context,
+                               const int32_t *page_table, int table_rows,
+                               int table_width, int heads, int kv_heads,
+                               int dim, int page_size, int64_t capacity,
+                               int window, float scale, const int32_t *plan,
+                               int plan_len, int32_t *flags, void *out,
+                               int phase, void *stream);
+
+/*
  * Entries of dd_prefill_attention's flags workspace for these arguments (0
  * when the call needs none); negative = -DD_E*.  No reference counterpart:
  * the exactness guard of the fp16 P.V product of bf16 pages.

@@ -360,3 +360,22 @@ def test_prefill_bf16_rerun_flags_fire_only_where_needed():
     exp = O.prefill_attention(q, case['cache_k'], cv, lengths, starts, slots, case['page_table'])
     exp_abs = O.prefill_attention(q, case['cache_k'], cv.abs(), lengths, starts, slots, case['page_table'])
     assert _relative_error(out, exp, exp_abs) <= 2e-3
+
+
+def test_prefill_phases_equal_one_call():
+    """dd_prefill_attention_phase 1 then 2 gives dd_prefill_attention's
+    output bit for bit, also when the re-run has items to redo."""
+    lengths, starts = [130, 40], [300, 0]
+    case, q, slots = build(lengths, starts, 16, 4, 128, torch.bfloat16, seed=13)
+    cv = case['cache_v'].clone()
+    cv[int(case['page_table'][0, 3]), 1, 5] = 2e5     # one item of segment 0 needs the re-run
+    table = case['page_table'].to(DEV)
+    packed = packing.pack_batch(lengths, starts, slots, table)
+    args = (q.to(DEV), case['cache_k'].to(DEV), cv.to(DEV), packed, table)
+    whole = ragged.prepare_prefill(*args).run().clone()
+    launch = ragged.prepare_prefill(*args)
+    launch.out.fill_(float('nan'))
+    launch.phase(1)
+    launch.phase(2)
+    assert torch.equal(launch.out, whole)
+    assert torch.isfinite(whole.float()).all()
