@@ -39,6 +39,7 @@
 #include "prefill_generic.h"
 
 #include <algorithm>
+#include <climits>
 #include <type_traits>
 #include <vector>
 
@@ -113,30 +114,19 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
   // each XCD with its own L2; every query tile of one (segment, KV head)
   // group is sent to the same XCD, longest first.  With a plan
   // (dd_prefill_plan) the host has chosen and balanced this order.
-  int grp, qt;
-  if (p.plan) {
-    const int item = p.plan[blockIdx.x];
-    if (item < 0) return;
-    grp = item / p.max_tiles;
-    qt = item - grp * p.max_tiles;
-  } else {
-    const int xcd = blockIdx.x & 7;
-    const int j = blockIdx.x >> 3;
-    grp = xcd + 8 * (j / p.max_tiles);
-    qt = p.max_tiles - 1 - j % p.max_tiles;
-  }
-  if (grp >= p.n * p.KH) return;
-  const int seg = grp / p.KH;
+  PrefillItem it;
+  if (!prefill_item(p, it)) return;
+  const int grp = it.grp, qt = it.qt, seg = it.seg;
   const int kh = grp - seg * p.KH;
-  const long tok0 = p.cu[seg];
-  const int len = (int)(p.cu[seg + 1] - tok0);
+  const long tok0 = it.tok0;
+  const int len = it.len;
   const int G = p.G;
   const int rows = COLS / G;
   const int r0 = qt * rows;
   if (r0 >= len) return;
-  const int context = (int)p.ctx[seg];
-  const int start = context - len;
-  const long slot = p.slots[seg];
+  const int start = it.start;
+  const int context = start + len;
+  const long slot = it.slot;
   const int rows_here = min(rows, len - r0);
 
   const int k_hi = start + r0 + rows_here;   // exclusive
@@ -657,11 +647,12 @@ extern "C" int dd_prefill_geometry(int dim, int *columns, int *keys_per_tile) {
 // visits plus a fixed start-up charge.  Groups (segment, KV head) are spread
 // over the 8 XCDs longest-processing-time first, so that every query tile of
 // a group shares one XCD's L2; within an XCD the items run longest first.
-// Workgroup b is dispatched to XCD b % 8, so plan[8 j + x] is the j-th item
-// of XCD x (-1 pads the shorter XCD lists).
-extern "C" int dd_prefill_plan(const int64_t *lengths, const int64_t *starts, int n, int heads, int kv_heads,
-                               int dim, int window, int32_t *plan, int capacity) {
-  if (!lengths || !starts || n < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || capacity < 0)
+// Workgroup b is dispatched to XCD b % 8, so entry 8 j + x is the j-th item
+// of XCD x (item -1 pads the shorter XCD lists).  An entry is kPlanInts
+// ints: the item, then its segment's token offset, length, start and slot.
+extern "C" int dd_prefill_plan(const int64_t *lengths, const int64_t *starts, const int64_t *slots, int n,
+                               int heads, int kv_heads, int dim, int window, int32_t *plan, int capacity) {
+  if (!lengths || !starts || !slots || n < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || capacity < 0)
     return -DD_EINVAL;
   Geometry g;
   if (!geometry(dim, &g)) return -DD_EUNSUPPORTED;
@@ -669,10 +660,15 @@ extern "C" int dd_prefill_plan(const int64_t *lengths, const int64_t *starts, in
   const int rows = g.cols / G;
   if (rows < 1) return -DD_EUNSUPPORTED;
   long max_len = 0;
+  std::vector<long> tok0(n + 1, 0);
   for (int i = 0; i < n; ++i) {
-    if (lengths[i] < 0 || starts[i] < 0) return -DD_EINVAL;
+    if (lengths[i] < 0 || starts[i] < 0 || lengths[i] + starts[i] > 0x7fffffffL || slots[i] < INT32_MIN ||
+        slots[i] > INT32_MAX)
+      return -DD_EINVAL;
     max_len = std::max<long>(max_len, lengths[i]);
+    tok0[i + 1] = tok0[i] + lengths[i];
   }
+  if (tok0[n] > 0x7fffffffL) return -DD_EUNSUPPORTED;
   const long max_tiles = dd_cdiv(max_len, rows);
   if ((long)n * kv_heads * std::max<long>(max_tiles, 1) > 0x7fffffffL) return -DD_EUNSUPPORTED;
   constexpr long kStartup = 2;  // charge of a workgroup's prologue and epilogue, in key tiles
@@ -713,6 +709,20 @@ extern "C" int dd_prefill_plan(const int64_t *lengths, const int64_t *starts, in
   if (need > 0x7fffffffL) return -DD_EUNSUPPORTED;
   if (!plan || capacity < need) return (int)need;
   for (size_t j = 0; j < longest; ++j)
-    for (int x = 0; x < kXcds; ++x) plan[kXcds * j + x] = j < lists[x].size() ? lists[x][j].second : -1;
+    for (int x = 0; x < kXcds; ++x) {
+      int32_t *e = plan + (long)kPlanInts * (kXcds * j + x);
+      for (int k = 0; k < kPlanInts; ++k) e[k] = 0;
+      if (j >= lists[x].size()) {
+        e[0] = -1;
+        continue;
+      }
+      const int item = lists[x][j].second;
+      const int seg = (int)(item / max_tiles) / kv_heads;
+      e[0] = item;
+      e[1] = (int32_t)tok0[seg];
+      e[2] = (int32_t)lengths[seg];
+      e[3] = (int32_t)starts[seg];
+      e[4] = (int32_t)slots[seg];
+    }
   return (int)need;
 }

@@ -28,7 +28,7 @@ struct PrefillParams {
   const int64_t *ctx;  // (n) start + len
   const int64_t *slots;
   const int32_t *table;
-  const int32_t *plan;  // optional: work item (group * max_tiles + qt) per workgroup, -1 = none
+  const int32_t *plan;  // optional: kPlanInts ints per workgroup (see PrefillItem), item -1 = none
   void *out;           // (T, H, D)
   long capacity;
   int n, max_tiles;
@@ -40,6 +40,46 @@ struct PrefillParams {
   unsigned q_sign;      // 0x80008000 when scale < 0: q enters negated (exact), so logits use |scale|
   int32_t *flags;       // bf16 pages, D 64/128: per work item, 1 = result must be recomputed exactly
 };
+
+// One work item of the prefill kernels: query tile qt of group grp =
+// (segment seg, KV head).  A plan entry (dd_prefill_plan) carries the item
+// and its segment's token offset, length, start and slot, so that a
+// workgroup reads them with one load instead of a chain of two.
+constexpr int kPlanInts = DD_PREFILL_PLAN_INTS;   // item, tok0, len, start, slot, 3 unused
+struct PrefillItem {
+  int grp, qt, seg, len, start;
+  long tok0, slot;
+};
+// false: the workgroup has nothing to do
+DD_DEV bool prefill_item(const PrefillParams &p, PrefillItem &it) {
+  if (p.plan) {
+    const int32_t *e = p.plan + (long)kPlanInts * blockIdx.x;
+    const int item = e[0];
+    if (item < 0) return false;
+    it.grp = item / p.max_tiles;
+    it.qt = item - it.grp * p.max_tiles;
+    it.seg = it.grp / p.KH;
+    it.tok0 = e[1];
+    it.len = e[2];
+    it.start = e[3];
+    it.slot = e[4];
+    return it.grp < p.n * p.KH;
+  }
+  // Without a plan: consecutive workgroups go to the 8 XCDs round-robin,
+  // each XCD with its own L2; every query tile of one (segment, KV head)
+  // group is sent to the same XCD, longest first.
+  const int xcd = blockIdx.x & 7;
+  const int j = blockIdx.x >> 3;
+  it.grp = xcd + 8 * (j / p.max_tiles);
+  it.qt = p.max_tiles - 1 - j % p.max_tiles;
+  if (it.grp >= p.n * p.KH) return false;
+  it.seg = it.grp / p.KH;
+  it.tok0 = p.cu[it.seg];
+  it.len = (int)(p.cu[it.seg + 1] - it.tok0);
+  it.start = (int)p.ctx[it.seg] - it.len;
+  it.slot = p.slots[it.seg];
+  return true;
+}
 
 template <int DT>
 DD_DEV f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {

@@ -178,31 +178,20 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   const int l32 = lane & 31;
   const int h2 = lane >> 5;
 
-  int grp, qt;
-  if (p.plan) {
-    const int item = p.plan[blockIdx.x];
-    if (item < 0) return;
-    grp = item / p.max_tiles;
-    qt = item - grp * p.max_tiles;
-  } else {
-    const int xcd = blockIdx.x & 7;
-    const int j = blockIdx.x >> 3;
-    grp = xcd + 8 * (j / p.max_tiles);
-    qt = p.max_tiles - 1 - j % p.max_tiles;
-  }
+  PrefillItem it;
+  if (!prefill_item(p, it)) return;
   __shared__ int s_flag;   // some column of this item needs the exact re-run
-  if (grp >= p.n * p.KH) return;
-  const int seg = grp / p.KH;
+  const int grp = it.grp, qt = it.qt, seg = it.seg;
   const int kh = grp - seg * p.KH;
-  const long tok0 = p.cu[seg];
-  const int len = (int)(p.cu[seg + 1] - tok0);
+  const long tok0 = it.tok0;
+  const int len = it.len;
   const int G = p.G;
   const int rows = COLS / G;
   const int r0 = qt * rows;
   if (r0 >= len) return;
-  const int context = (int)p.ctx[seg];
-  const int start = context - len;
-  const long slot = p.slots[seg];
+  const int start = it.start;
+  const int context = start + len;
+  const long slot = it.slot;
   const int rows_here = min(rows, len - r0);
 
   const int k_hi = start + r0 + rows_here;  // exclusive

@@ -42,27 +42,34 @@ def _has_mfma_geometry(dim):
     return _native.library().dd_prefill_geometry(int(dim), ctypes.byref(cols), ctypes.byref(keys)) == 0
 
 
-def prefill_plan(lengths, starts, heads, kv_heads, dim, window=0):
-    """Workgroup order of the prefill kernel for these segments (host int32).
+def prefill_plan(lengths, starts, heads, kv_heads, dim, window=0, slots=None):
+    """Workgroup order of the prefill kernel for these segments: a host int32
+    array (entries, 8), each row (item or -1, first packed token, length,
+    start, slot, 0, 0, 0).
 
     Balances (segment, KV head, query tile) items over the XCDs, longest
-    first, from the host copies of the segment lengths and starts.
+    first, from the host copies of the segment lengths, starts and slots
+    (slots default to 0 .. n-1).
     """
     lengths = np.ascontiguousarray(lengths, dtype=np.int64)
     starts = np.ascontiguousarray(starts, dtype=np.int64)
-    if lengths.shape != starts.shape or lengths.ndim != 1:
-        raise ValueError('lengths and starts must be matching 1-D sequences')
+    slots = np.ascontiguousarray(np.arange(len(lengths)) if slots is None else slots, dtype=np.int64)
+    if lengths.shape != starts.shape or lengths.shape != slots.shape or lengths.ndim != 1:
+        raise ValueError('lengths, starts and slots must be matching 1-D sequences')
     lib = _native.library()
-    args = (lengths.ctypes.data_as(ctypes.c_void_p), starts.ctypes.data_as(ctypes.c_void_p), len(lengths),
-            heads, kv_heads, dim, int(window or 0))
+    args = (lengths.ctypes.data_as(ctypes.c_void_p), starts.ctypes.data_as(ctypes.c_void_p),
+            slots.ctypes.data_as(ctypes.c_void_p), len(lengths), heads, kv_heads, dim, int(window or 0))
     need = lib.dd_prefill_plan(*args, None, 0)
     if need < 0:
         raise _native.NativeError(f'dd_prefill_plan failed: {lib.dd_error_string(-need).decode()} ({-need})')
-    plan = np.empty(max(need, 1), dtype=np.int32)
+    plan = np.empty((max(need, 1), PLAN_INTS), dtype=np.int32)
     got = lib.dd_prefill_plan(*args, plan.ctypes.data_as(ctypes.c_void_p), len(plan))
     if got != need:
         raise _native.NativeError('dd_prefill_plan returned an inconsistent length')
     return plan[:need]
+
+
+PLAN_INTS = 8   # DD_PREFILL_PLAN_INTS
 
 
 def prefill_attention(query, cache_k, cache_v, packed, page_table, window=0, scale=None, out=None,
@@ -105,7 +112,8 @@ def prepare_prefill(query, cache_k, cache_v, packed, page_table, window=0, scale
     if q.dtype != torch.float32 and scale != 0.0 and _has_mfma_geometry(D):
         # the MFMA kernel's XCD-balanced workgroup order (the fp32 / other-D
         # kernel takes none)
-        plan = prefill_plan(packed.lengths[a:b], packed.starts[a:b], H, cache_k.shape[1], D, window)
+        plan = prefill_plan(packed.lengths[a:b], packed.starts[a:b], H, cache_k.shape[1], D, window,
+                            packed.slots[a:b])
         if len(plan) == 0:
             return PrefillLaunch(out, None)
         plan_dev = _native.upload(torch.from_numpy(plan), q.device)

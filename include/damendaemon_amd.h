@@ -261,8 +261,8 @@ int dd_rope_batch(const void *qkv, int qkv_dtype, const void *cos,
  *   scale         any finite value (non-finite: DD_EINVAL); 0 gives uniform
  *                 weights over each row's allowed keys, as SDPA does
  *   plan          NULL, or the device copy of dd_prefill_plan's output for
- *                 these same lengths/starts (plan_len entries): the
- *                 workgroup order; NULL uses a fixed XCD-aware order
+ *                 these same segments (plan_len entries): the workgroup
+ *                 order; NULL uses a fixed XCD-aware order
  *   flags         device int32 workspace of dd_prefill_flag_count(...)
  *                 entries (NULL allowed when that count is 0).  The bf16
  *                 kernel at dim 64/128 multiplies V in fp16; a work item
@@ -309,14 +309,18 @@ int dd_prefill_flag_count(int n, int max_len, int heads, int kv_heads,
 
 /*
  * Host-side schedule for dd_prefill_attention (no reference counterpart:
- * the reference runs one SDPA per segment, paged.py:97-111).  lengths and
- * starts are HOST int64 arrays (n).  Writes the workgroup order to plan
- * (host int32, capacity entries) and returns its length; with plan == NULL
- * or too small a capacity it only returns the length.  Negative = -DD_E*.
+ * the reference runs one SDPA per segment, paged.py:97-111).  lengths,
+ * starts and slots are HOST int64 arrays (n), the same segments as the
+ * call's device metadata.  Writes the workgroup order to plan (host int32,
+ * DD_PREFILL_PLAN_INTS per entry, capacity entries): each entry holds the
+ * work item (-1: none) and its segment's first packed token, length, start
+ * and slot.  Returns the number of entries; with plan == NULL or too small
+ * a capacity it only returns that number.  Negative = -DD_E*.
  */
-int dd_prefill_plan(const int64_t *lengths, const int64_t *starts, int n,
-                    int heads, int kv_heads, int dim, int window,
-                    int32_t *plan, int capacity);
+#define DD_PREFILL_PLAN_INTS 8
+int dd_prefill_plan(const int64_t *lengths, const int64_t *starts,
+                    const int64_t *slots, int n, int heads, int kv_heads,
+                    int dim, int window, int32_t *plan, int capacity);
 
 /*
  * Tile geometry of dd_prefill_attention for head size dim: (query row,

@@ -33,11 +33,21 @@ int main(void) {
   /* plan for 3 segments (two chunks and a short one) over 8 KV heads */
   const int64_t lengths[3] = {512, 300, 17};
   const int64_t starts[3] = {4000, 0, 900};
-  const int need = dd_prefill_plan(lengths, starts, 3, 32, 8, 128, 0, NULL, 0);
+  const int64_t slots[3] = {5, 2, 7};
+  const int need = dd_prefill_plan(lengths, starts, slots, 3, 32, 8, 128, 0, NULL, 0);
   CHECK(need > 0 && need % 8 == 0);
+  static int32_t entries[4096 * DD_PREFILL_PLAN_INTS];
   int32_t plan[4096];
   CHECK(need <= 4096);
-  CHECK(dd_prefill_plan(lengths, starts, 3, 32, 8, 128, 0, plan, need) == need);
+  CHECK(dd_prefill_plan(lengths, starts, slots, 3, 32, 8, 128, 0, entries, need) == need);
+  for (int i = 0; i < need; ++i) {
+    const int32_t *e = entries + (long)i * DD_PREFILL_PLAN_INTS;
+    plan[i] = e[0];
+    if (e[0] < 0) continue;
+    const int seg = e[0] / ((512 + cols / 4 - 1) / (cols / 4)) / 8;
+    CHECK(e[2] == lengths[seg] && e[3] == starts[seg] && e[4] == slots[seg]);
+    CHECK(e[1] == (seg == 0 ? 0 : seg == 1 ? 512 : 812));
+  }
   /* every (segment, KV head, query tile) item appears exactly once */
   const int rows = cols / 4;
   const int max_tiles = (512 + rows - 1) / rows;

@@ -44,9 +44,15 @@ def test_plan_covers_every_tile_once_grouped_per_xcd_longest_first(seed):
     lengths = [rng.choice([1, 7, 64, 300, 512, 1000]) for _ in range(n)]
     starts = [rng.randint(0, 5000) for _ in range(n)]
     window = rng.choice([0, 0, 700])
-    plan = ragged.prefill_plan(lengths, starts, heads, kv_heads, dim, window)
+    entries = ragged.prefill_plan(lengths, starts, heads, kv_heads, dim, window)
+    plan = entries[:, 0]
     cost, max_tiles = _items(lengths, starts, heads, kv_heads, dim, window)
-    assert plan.dtype == np.int32 and len(plan) % 8 == 0
+    assert entries.dtype == np.int32 and entries.shape[1] == 8 and len(plan) % 8 == 0
+    # each entry carries its segment's packed offset, length, start and slot
+    tok0 = np.concatenate([[0], np.cumsum(lengths)])
+    for e in entries[plan >= 0]:
+        seg = int(e[0]) // max_tiles // kv_heads
+        assert list(e[1:5]) == [tok0[seg], lengths[seg], starts[seg], seg] and not e[5:].any()
     real = plan[plan >= 0].tolist()
     assert sorted(real) == sorted(cost)             # every item exactly once
     xcd_of_group = {}
@@ -68,7 +74,7 @@ def test_plan_covers_every_tile_once_grouped_per_xcd_longest_first(seed):
 def test_plan_balances_xcds():
     lengths = [512] * 8
     starts = [3198, 2211, 2253, 3990, 2141, 2468, 3884, 968]
-    plan = ragged.prefill_plan(lengths, starts, 32, 8, 128, 0)
+    plan = ragged.prefill_plan(lengths, starts, 32, 8, 128, 0)[:, 0]
     cost, _ = _items(lengths, starts, 32, 8, 128, 0)
     loads = [sum(cost[i] for i in plan[x::8] if i >= 0) for x in range(8)]
     assert max(loads) <= 1.2 * min(loads)
