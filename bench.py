@@ -212,7 +212,7 @@ def main():
 
     # Kernel timing: the split kernel and the merge bracketed by HIP events on
     # the launch stream (torch's current stream), K launches.
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     for e0, e1, e2 in events:
         e0.record()
         launch.partials()
