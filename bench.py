@@ -416,7 +416,7 @@ def bench_rope(args, dev):
                      'C4 packed batch through rope_batch: 4,216 tokens (8 x 512 prefill + 120 decode), '
                      'H32/KH8/D128, rotary dim 128, page 16; 4 independent batches used in turn', 'rope',
                      {'bytes_per_token': per_token, 'rotated_sets': ROTATE})
-    line['roofline']['traffic'] = measured_traffic('rope_c4_pmc', 'rope')
+    line['roofline']['traffic'] = measured_traffic('rope_c4_kernel_trace', 'rope')
     print(json.dumps(line), flush=True)
 
 
@@ -458,7 +458,7 @@ def bench_copy(args, dev):
                      '4 independent pools used in turn', 'copy',
                      {'restore_ms': restore_ms, 'rotated_sets': ROTATE,
                       'restore_hbm_gbps': nbytes / (restore_ms * 1e-3) / 1e9})
-    line['roofline']['traffic'] = measured_traffic('copy_pages_pmc', 'copy')
+    line['roofline']['traffic'] = measured_traffic('copy_pages_kernel_trace', 'copy')
     print(json.dumps(line), flush=True)
 
 
