@@ -301,8 +301,7 @@ def bench_mixed(args, dev, dtype=torch.bfloat16):
         if decode_rows:
             kernels.prepare_attention(case['q'][t_prefill:].unsqueeze(2), ck, cv, packed.positions[t_prefill:],
                                       packed.slot_ids[t_prefill:], page_table=table,
-                                      out=out[t_prefill:].unsqueeze(2),
-                                      work=kernels.stream_work_counter(dev)).run()
+                                      out=out[t_prefill:].unsqueeze(2)).run()
         if ev:
             ev[2].record()
         return out

@@ -33,7 +33,7 @@ SIGNATURES = {
                             _p, _p, _p, _i, _i,               # positions, slots, table, rows, width
                             _i, _i, _i, _i, _i, _i64, _i, _f,  # B H KH D page cap window scale
                             _p, _p, _i, _f, _p,               # alibi rel buckets denom sinks
-                            _p, _p, _p, _i, _i, _p, _p],      # out part lse splits split_tokens work stream
+                            _p, _p, _p, _i, _i, _p],          # out part lse splits split_tokens stream
 }
 SIGNATURES['dd_quantize_q8'] = [_p, _i, _i64, _i, _i, _p, _p, _p]
 SIGNATURES['dd_dequantize_q8'] = [_p, _p, _i64, _i, _i, _p, _i, _p]
@@ -54,7 +54,7 @@ SIGNATURES['dd_ring_decode_indices'] = [_p, _i64, _i, _i, _i, _p, _p]
 SIGNATURES['dd_decode_partials'] = SIGNATURES['dd_decode_attention']
 SIGNATURES['dd_decode_merge'] = SIGNATURES['dd_decode_attention']
 # the allocation-free variant: no partial / lse arguments
-SIGNATURES['dd_decode_attention_static'] = SIGNATURES['dd_decode_attention'][:-6] + [_i, _i, _p]
+SIGNATURES['dd_decode_attention_static'] = SIGNATURES['dd_decode_attention'][:-5] + [_i, _i, _p]
 
 
 class NativeError(RuntimeError):

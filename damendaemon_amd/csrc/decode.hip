@@ -45,8 +45,7 @@ static int decode_entry(int phase, const void *q, int q_dtype, const void *k, co
                                    int table_rows, int table_width, int batch, int heads, int kv_heads, int dim, int page_size,
                                    int64_t capacity, int window, float scale, const float *alibi, const float *rel_bias,
                                    int rel_buckets, float rel_denom, const float *sinks, void *out,
-                                   float *partial, float *lse, int splits, int split_tokens, int32_t *work,
-                                   void *stream) {
+                                   float *partial, float *lse, int splits, int split_tokens, void *stream) {
   if (!q || !k || !v || !positions || !out || batch < 0 || capacity <= 0 || heads <= 0 || kv_heads <= 0 ||
       heads % kv_heads || page_size <= 0 || splits <= 0 || split_tokens <= 0 || split_tokens % 64)
     return DD_EINVAL;
@@ -64,7 +63,6 @@ static int decode_entry(int phase, const void *q, int q_dtype, const void *k, co
   p.out = out;
   p.part = partial;
   p.lse = lse;
-  p.work = work;
   p.alibi = alibi;
   p.rel = rel_bias;
   p.sinks = sinks;
@@ -116,9 +114,8 @@ extern "C" int dd_decode_attention(const void *q, int q_dtype, const void *k, co
                                    int table_rows, int table_width, int batch, int heads, int kv_heads, int dim, int page_size,
                                    int64_t capacity, int window, float scale, const float *alibi, const float *rel_bias,
                                    int rel_buckets, float rel_denom, const float *sinks, void *out,
-                                   float *partial, float *lse, int splits, int split_tokens, int32_t *work,
-                                   void *stream) {
-  return decode_entry(3, q, q_dtype, k, v, kv_dtype, k_scale, v_scale, group, positions, slots, page_table, table_rows, table_width, batch, heads, kv_heads, dim, page_size, capacity, window, scale, alibi, rel_bias, rel_buckets, rel_denom, sinks, out, partial, lse, splits, split_tokens, work, stream);
+                                   float *partial, float *lse, int splits, int split_tokens, void *stream) {
+  return decode_entry(3, q, q_dtype, k, v, kv_dtype, k_scale, v_scale, group, positions, slots, page_table, table_rows, table_width, batch, heads, kv_heads, dim, page_size, capacity, window, scale, alibi, rel_bias, rel_buckets, rel_denom, sinks, out, partial, lse, splits, split_tokens, stream);
 }
 
 extern "C" int dd_decode_partials(const void *q, int q_dtype, const void *k, const void *v, int kv_dtype,
@@ -127,9 +124,8 @@ extern "C" int dd_decode_partials(const void *q, int q_dtype, const void *k, con
                                    int table_rows, int table_width, int batch, int heads, int kv_heads, int dim, int page_size,
                                    int64_t capacity, int window, float scale, const float *alibi, const float *rel_bias,
                                    int rel_buckets, float rel_denom, const float *sinks, void *out,
-                                   float *partial, float *lse, int splits, int split_tokens, int32_t *work,
-                                   void *stream) {
-  return decode_entry(1, q, q_dtype, k, v, kv_dtype, k_scale, v_scale, group, positions, slots, page_table, table_rows, table_width, batch, heads, kv_heads, dim, page_size, capacity, window, scale, alibi, rel_bias, rel_buckets, rel_denom, sinks, out, partial, lse, splits, split_tokens, work, stream);
+                                   float *partial, float *lse, int splits, int split_tokens, void *stream) {
+  return decode_entry(1, q, q_dtype, k, v, kv_dtype, k_scale, v_scale, group, positions, slots, page_table, table_rows, table_width, batch, heads, kv_heads, dim, page_size, capacity, window, scale, alibi, rel_bias, rel_buckets, rel_denom, sinks, out, partial, lse, splits, split_tokens, stream);
 }
 
 extern "C" int dd_decode_merge(const void *q, int q_dtype, const void *k, const void *v, int kv_dtype,
@@ -138,9 +134,8 @@ extern "C" int dd_decode_merge(const void *q, int q_dtype, const void *k, const 
                                    int table_rows, int table_width, int batch, int heads, int kv_heads, int dim, int page_size,
                                    int64_t capacity, int window, float scale, const float *alibi, const float *rel_bias,
                                    int rel_buckets, float rel_denom, const float *sinks, void *out,
-                                   float *partial, float *lse, int splits, int split_tokens, int32_t *work,
-                                   void *stream) {
-  return decode_entry(2, q, q_dtype, k, v, kv_dtype, k_scale, v_scale, group, positions, slots, page_table, table_rows, table_width, batch, heads, kv_heads, dim, page_size, capacity, window, scale, alibi, rel_bias, rel_buckets, rel_denom, sinks, out, partial, lse, splits, split_tokens, work, stream);
+                                   float *partial, float *lse, int splits, int split_tokens, void *stream) {
+  return decode_entry(2, q, q_dtype, k, v, kv_dtype, k_scale, v_scale, group, positions, slots, page_table, table_rows, table_width, batch, heads, kv_heads, dim, page_size, capacity, window, scale, alibi, rel_bias, rel_buckets, rel_denom, sinks, out, partial, lse, splits, split_tokens, stream);
 }
 
 // ---- allocation-free variant ----------------------------------------------
@@ -192,19 +187,15 @@ extern "C" int dd_decode_attention_static(const void *q, int q_dtype, const void
   // partials (batch*heads, splits, dim) then lse (batch*heads, splits)
   const long rows = (long)batch * heads * splits;
   const long need = rows * (dim + 1L);
-  // the last 64 floats hold the work counter (zero at load, left at zero by
-  // every call)
-  if (splits > 1 && need > (long)DD_STATIC_SCRATCH_FLOATS - 64) return DD_ESCRATCH;
+  if (splits > 1 && need > (long)DD_STATIC_SCRATCH_FLOATS) return DD_ESCRATCH;
   float *part = nullptr, *lse = nullptr;
-  int32_t *work = nullptr;
   if (splits > 1 && batch > 0) {
     float *base = static_scratch((hipStream_t)stream);
     if (!base) return DD_ELAUNCH;
     part = base;
     lse = base + rows * dim;
-    work = (int32_t *)(base + DD_STATIC_SCRATCH_FLOATS - 64);
   }
   return decode_entry(3, q, q_dtype, k, v, kv_dtype, k_scale, v_scale, group, positions, slots, page_table,
                       table_rows, table_width, batch, heads, kv_heads, dim, page_size, capacity, window, scale,
-                      alibi, rel_bias, rel_buckets, rel_denom, sinks, out, part, lse, splits, split_tokens, work, stream);
+                      alibi, rel_bias, rel_buckets, rel_denom, sinks, out, part, lse, splits, split_tokens, stream);
 }

@@ -58,11 +58,6 @@ struct DecodeParams {
   int paged;
   int chunk_shift;  // log2(page / 16) for paged caches
   int xcd_units;   // int8 pages: KV heads whose scale blocks share one 128-byte line (1 = no remap)
-  // Work counter of the split kernel's dynamic schedule (NULL: one unit per
-  // workgroup).  Zero when the split kernel starts; the merge kernel of the
-  // same call sets it back to zero.
-  int *work;
-  int resident;   // workgroups launched under the dynamic schedule
 };
 
 // Workgroup id -> logical (split, sequence, KV head) index for the int8
@@ -652,9 +647,6 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int D) {
     }
     store_as<QT>(p.out, bh * D + d, o / den);
   }
-  // every split workgroup has finished (stream order): the counter goes back
-  // to zero for the next call
-  if (p.work && blockIdx.x == 0 && threadIdx.x == 0) atomicExch(p.work, 0);
 }
 
 // phase bit 1: split kernel; bit 2: merge kernel (only when splits > 1).

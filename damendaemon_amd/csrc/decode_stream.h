@@ -327,382 +327,337 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
 
   // Workgroup (split, sequence, KV head, head group): with more than 16
   // query heads per KV head, gsub workgroups of up to 16 heads each.
-  // One unit of work: workgroup index wg of the static schedule (split,
-  // sequence, KV head, head group), split-major.
-  auto unit = [&](const int wg) __attribute__((always_inline)) {
-    const int per_b = p.KH * p.gsub;
-    const int nbkh = p.B * per_b;
-    const int split = wg / nbkh;
-    const int bkh = wg - split * nbkh;
-    const int b = bkh / per_b;
-    const int vk = bkh - b * per_b;
-    const int kh = vk / p.gsub;
-    const int gofs = 16 * (vk - kh * p.gsub);   // first head of this workgroup within the group
-    const int G = p.gsub > 1 ? min(16, p.G - gofs) : p.G;   // heads of this workgroup
+  const int wg = blockIdx.x;
+  const int per_b = p.KH * p.gsub;
+  const int nbkh = p.B * per_b;
+  const int split = wg / nbkh;
+  const int bkh = wg - split * nbkh;
+  const int b = bkh / per_b;
+  const int vk = bkh - b * per_b;
+  const int kh = vk / p.gsub;
+  const int gofs = 16 * (vk - kh * p.gsub);   // first head of this workgroup within the group
+  const int G = p.gsub > 1 ? min(16, p.G - gofs) : p.G;   // heads of this workgroup
 
-    const long pos64 = p.pos[b];
-    const int row = p.slots ? (int)p.slots[b] : 0;
-    const int t_hi = pos64 + 1 < p.ctx_limit ? (int)pos64 + 1 : p.ctx_limit;
-    int t_lo = 0;
-    if (p.window > 0 && pos64 - p.window + 1 > 0) t_lo = (int)(pos64 - p.window + 1);
-    int s_lo = split * p.split_tokens;
-    int s_hi = s_lo + p.split_tokens;
-    if (s_hi > t_hi) s_hi = t_hi;
-    if (s_lo < t_lo) s_lo = t_lo;
-    if (s_lo >= s_hi) return;  // empty split: the merge never reads it
-    const int pg_first = s_lo >> 4;
-    const int pg_last = (s_hi - 1) >> 4;
-    const long head0 = (long)b * p.H + (long)kh * p.G + gofs;
-    const bool col_on = n16 < G;
+  const long pos64 = p.pos[b];
+  const int row = p.slots ? (int)p.slots[b] : 0;
+  const int t_hi = pos64 + 1 < p.ctx_limit ? (int)pos64 + 1 : p.ctx_limit;
+  int t_lo = 0;
+  if (p.window > 0 && pos64 - p.window + 1 > 0) t_lo = (int)(pos64 - p.window + 1);
+  int s_lo = split * p.split_tokens;
+  int s_hi = s_lo + p.split_tokens;
+  if (s_hi > t_hi) s_hi = t_hi;
+  if (s_lo < t_lo) s_lo = t_lo;
+  if (s_lo >= s_hi) return;  // empty split: the merge never reads it
+  const int pg_first = s_lo >> 4;
+  const int pg_last = (s_hi - 1) >> 4;
+  const long head0 = (long)b * p.H + (long)kh * p.G + gofs;
+  const bool col_on = n16 < G;
 
-    // Q^T operand: lane (head n16, dims 8kg + 32c ..+8); fp32: dims
-    // (D/4) kg + 4c ..+4, one v_mfma_f32_16x16x4_f32 per dim of the four.
-    u32x4 qa[NC];
-    if constexpr (F32) {
-      const float *qf = (const float *)p.q;
-  #pragma unroll
-      for (int c = 0; c < NC; ++c)
-        qa[c] = col_on ? *(const u32x4 *)(qf + (head0 + n16) * D + (D / 4) * kg + 4 * c) : u32x4{0, 0, 0, 0};
-    } else {
-      const unsigned short *qb = (const unsigned short *)p.q;
-  #pragma unroll
-      for (int c = 0; c < NC; ++c)
-        qa[c] = col_on ? *(const u32x4 *)(qb + (head0 + n16) * D + 8 * kg + 32 * c) : u32x4{0, 0, 0, 0};
-    }
-    float slope = (p.alibi && col_on) ? p.alibi[(long)kh * p.G + gofs + n16] * kLog2e : 0.f;
-
-    // Per-lane LDS byte offsets (loop invariant).
-    const unsigned wbase = (unsigned)(size_t)(lds_void *)s_ring + (unsigned)(w * NB * STAGE);
-    unsigned dma_off[IPP];
-  #pragma unroll
-    for (int j = 0; j < IPP; ++j) {
-      const int e = 64 * j + lane;
-      if constexpr (PADR) {
-        const int r = e / SPR, c = e % SPR;
-        dma_off[j] = r < 16 && c < CPR ? (unsigned)(r * ROWB + 16 * c) : 0x40000000u;
-      } else {
-        const int r = e / CPR;
-        dma_off[j] = (unsigned)(r * ROWB + 16 * ((e % CPR) ^ stream_swz_of<DT, D>(r)));
-      }
-    }
-    unsigned k_addr[NC];
-  #pragma unroll
+  // Q^T operand: lane (head n16, dims 8kg + 32c ..+8); fp32: dims
+  // (D/4) kg + 4c ..+4, one v_mfma_f32_16x16x4_f32 per dim of the four.
+  u32x4 qa[NC];
+  if constexpr (F32) {
+    const float *qf = (const float *)p.q;
+#pragma unroll
     for (int c = 0; c < NC; ++c)
-      k_addr[c] = wbase + n16 * RSB + 16 * ((F32 ? (D / 16) * kg + c : 4 * c + kg) ^ stream_swz_of<DT, D>(n16));
-    // V^T operand.  16-bit: transposing reads (lane: 4 keys of one dim per
-    // tile).  fp32: O^T tile md, row m holds dim MD m + md, so that lane
-    // (kg, n16) reads the MD contiguous dims MD n16 .. of key 4 kg + e
-    // (MD / 4 reads of 16 bytes per key, address index e (MD / 4) + q).
-    constexpr bool V8 = F32 && MD % 4 != 0;   // fp32 V read 8 bytes at a time (D = 96)
-    unsigned v_addr[V8 ? 2 * MD : MD];
-    if constexpr (V8) {
-  #pragma unroll
-      for (int e = 0; e < 4; ++e)
-  #pragma unroll
-        for (int q = 0; q < MD / 2; ++q) {
-          const int r = 4 * kg + e;
-          v_addr[e * (MD / 2) + q] = wbase + PAGEB + r * RSB + 4 * (MD * n16 + 2 * q);
-        }
-    } else if constexpr (F32) {
-  #pragma unroll
-      for (int e = 0; e < 4; ++e)
-  #pragma unroll
-        for (int q = 0; q < MD / 4; ++q) {
-          const int r = 4 * kg + e;
-          v_addr[e * (MD / 4) + q] =
-              wbase + PAGEB + r * RSB + 16 * (((MD / 4) * n16 + q) ^ stream_swz_of<DT, D>(r));
-        }
+      qa[c] = col_on ? *(const u32x4 *)(qf + (head0 + n16) * D + (D / 4) * kg + 4 * c) : u32x4{0, 0, 0, 0};
+  } else {
+    const unsigned short *qb = (const unsigned short *)p.q;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      qa[c] = col_on ? *(const u32x4 *)(qb + (head0 + n16) * D + 8 * kg + 32 * c) : u32x4{0, 0, 0, 0};
+  }
+  float slope = (p.alibi && col_on) ? p.alibi[(long)kh * p.G + gofs + n16] * kLog2e : 0.f;
+
+  // Per-lane LDS byte offsets (loop invariant).
+  const unsigned wbase = (unsigned)(size_t)(lds_void *)s_ring + (unsigned)(w * NB * STAGE);
+  unsigned dma_off[IPP];
+#pragma unroll
+  for (int j = 0; j < IPP; ++j) {
+    const int e = 64 * j + lane;
+    if constexpr (PADR) {
+      const int r = e / SPR, c = e % SPR;
+      dma_off[j] = r < 16 && c < CPR ? (unsigned)(r * ROWB + 16 * c) : 0x40000000u;
     } else {
-      const int a = lane & 15;
-      const int r = 4 * kg + (a >> 2);
-      const int q = a & 3;
-  #pragma unroll
-      for (int md = 0; md < MD; ++md)
-        v_addr[md] = wbase + PAGEB + r * RSB + 16 * ((2 * md + (q >> 1)) ^ stream_swz_of<DT, D>(r)) + 8 * (q & 1);
+      const int r = e / CPR;
+      dma_off[j] = (unsigned)(r * ROWB + 16 * ((e % CPR) ^ stream_swz_of<DT, D>(r)));
+    }
+  }
+  unsigned k_addr[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+    k_addr[c] = wbase + n16 * RSB + 16 * ((F32 ? (D / 16) * kg + c : 4 * c + kg) ^ stream_swz_of<DT, D>(n16));
+  // V^T operand.  16-bit: transposing reads (lane: 4 keys of one dim per
+  // tile).  fp32: O^T tile md, row m holds dim MD m + md, so that lane
+  // (kg, n16) reads the MD contiguous dims MD n16 .. of key 4 kg + e
+  // (MD / 4 reads of 16 bytes per key, address index e (MD / 4) + q).
+  constexpr bool V8 = F32 && MD % 4 != 0;   // fp32 V read 8 bytes at a time (D = 96)
+  unsigned v_addr[V8 ? 2 * MD : MD];
+  if constexpr (V8) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int q = 0; q < MD / 2; ++q) {
+        const int r = 4 * kg + e;
+        v_addr[e * (MD / 2) + q] = wbase + PAGEB + r * RSB + 4 * (MD * n16 + 2 * q);
+      }
+  } else if constexpr (F32) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int q = 0; q < MD / 4; ++q) {
+        const int r = 4 * kg + e;
+        v_addr[e * (MD / 4) + q] =
+            wbase + PAGEB + r * RSB + 16 * (((MD / 4) * n16 + q) ^ stream_swz_of<DT, D>(r));
+      }
+  } else {
+    const int a = lane & 15;
+    const int r = 4 * kg + (a >> 2);
+    const int q = a & 3;
+#pragma unroll
+    for (int md = 0; md < MD; ++md)
+      v_addr[md] = wbase + PAGEB + r * RSB + 16 * ((2 * md + (q >> 1)) ^ stream_swz_of<DT, D>(r)) + 8 * (q & 1);
+  }
+
+  // This wave's chunks: first + i * NW, i < n.
+  const int first = pg_first + w;
+  const int n = first <= pg_last ? (pg_last - first) / NW + 1 : 0;
+
+  const char *kplane = (const char *)p.k;
+  const char *vplane = (const char *)p.v;
+  const __attribute__((address_space(4))) int32_t *tab = (const __attribute__((address_space(4))) int32_t *)p.table;
+  // Buffer resources of chunk i of this wave (K, V).  Chunks past the wave's
+  // last one get an empty resource (no memory traffic): every iteration then
+  // has the same loads in flight and waits for a constant count.
+  struct ChunkRsrc {
+    __amdgpu_buffer_rsrc_t k, v;
+  };
+  auto chunk_rsrc = [&](int i) __attribute__((always_inline)) -> ChunkRsrc {
+    const int pg = first + i * NW;
+    long base;  // element offset of the chunk's first row, -1 when unmapped
+    if (i >= n) {
+      base = -1;
+    } else if (p.paged) {
+      base = -1;
+      if (row >= 0 && row < p.table_rows) {
+        const int entry = pg >> p.chunk_shift;
+        const long phys = tab[(long)row * p.table_w + entry];
+        if (phys >= 0 && phys < p.capacity)
+          base = ((phys * p.KH + kh) * (long)p.page + ((pg - (entry << p.chunk_shift)) << 4)) * (long)D;
+      }
+    } else {
+      base = (row >= 0 && row < p.capacity) ? (((long)row * p.KH + kh) * (long)p.page + (long)pg * 16) * (long)D : -1;
+    }
+    base = (long)uniform_ptr((const char *)base);
+    const int live = base < 0 ? 0 : max(0, min(16, s_hi - pg * 16));
+    const long off = base < 0 ? 0 : (F32 ? 4 : 2) * base;
+    const int bytes = uniform(live * ROWB);
+    return ChunkRsrc{
+        __builtin_amdgcn_make_buffer_rsrc((void *)uniform_ptr(kplane + off), (short)0, bytes, kRawBufferWord3),
+        __builtin_amdgcn_make_buffer_rsrc((void *)uniform_ptr(vplane + off), (short)0, bytes, kRawBufferWord3)};
+  };
+  // Chunk i straight into LDS `stage` (direct-to-LDS loads).
+  auto issue = [&](int i, int stage) __attribute__((always_inline)) {
+    const ChunkRsrc r = chunk_rsrc(i);
+    char *dst = s_ring + (w * NB + stage) * STAGE;
+#pragma unroll
+    for (int j = 0; j < IPP; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r.k, (lds_void *)(dst + 1024 * j), 16, dma_off[j], 0, 0,
+                                               kStreamLoadAux);
+#pragma unroll
+    for (int j = 0; j < IPP; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r.v, (lds_void *)(dst + PAGEB + 1024 * j), 16, dma_off[j], 0, 0,
+                                               kStreamLoadAux);
+  };
+
+  f32x4 o[MD];
+#pragma unroll
+  for (int md = 0; md < MD; ++md) o[md] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegInf;  // running max of this lane's head (log2 domain)
+  float lsum = 0.f;       // this lane's share of the running denominator
+
+  auto consume = [&](int i, auto stage_tag) __attribute__((always_inline)) {
+    constexpr int SOFF = decltype(stage_tag)::value * STAGE;
+    const int t0 = (first + i * NW) * 16;
+    u32x4 ka[NC];
+    u32x2 va[F32 ? 1 : MD];
+    u32x4 vf[F32 && !V8 ? MD : 1];
+    u32x2 vh[V8 ? 2 * MD : 1];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) ka[c] = lds_read_b128<SOFF>(k_addr[c]);
+    if constexpr (V8) {
+#pragma unroll
+      for (int j = 0; j < 2 * MD; ++j) vh[j] = lds_read_b64<SOFF>(v_addr[j]);
+    } else {
+#pragma unroll
+      for (int md = 0; md < MD; ++md) {
+        if constexpr (F32) {
+          vf[md] = lds_read_b128<SOFF>(v_addr[md]);
+        } else {
+          va[md] = lds_read_tr16<SOFF>(v_addr[md]);
+        }
+      }
+    }
+    wait_lds();
+#pragma unroll
+    for (int c = 0; c < NC; ++c) after_wait(ka[c]);
+    if constexpr (V8) {
+#pragma unroll
+      for (int j = 0; j < 2 * MD; ++j) after_wait(vh[j]);
+    } else {
+#pragma unroll
+      for (int md = 0; md < MD; ++md) {
+        if constexpr (F32) {
+          after_wait(vf[md]);
+        } else {
+          after_wait(va[md]);
+        }
+      }
+    }
+    // The stage is in registers now: refill it with chunk i + NB.
+    issue(i + NB, decltype(stage_tag)::value);
+
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (F32) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          s = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(ka[c][q]), __uint_as_float(qa[c][q]), s, 0, 0,
+                                                   0);
+    } else {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) s = mfma16x16x32<DT>(ka[c], qa[c], s);
     }
 
-    // This wave's chunks: first + i * NW, i < n.
-    const int first = pg_first + w;
-    const int n = first <= pg_last ? (pg_last - first) / NW + 1 : 0;
-
-    const char *kplane = (const char *)p.k;
-    const char *vplane = (const char *)p.v;
-    const __attribute__((address_space(4))) int32_t *tab = (const __attribute__((address_space(4))) int32_t *)p.table;
-    // Buffer resources of chunk i of this wave (K, V).  Chunks past the wave's
-    // last one get an empty resource (no memory traffic): every iteration then
-    // has the same loads in flight and waits for a constant count.
-    struct ChunkRsrc {
-      __amdgpu_buffer_rsrc_t k, v;
-    };
-    auto chunk_rsrc = [&](int i) __attribute__((always_inline)) -> ChunkRsrc {
-      const int pg = first + i * NW;
-      long base;  // element offset of the chunk's first row, -1 when unmapped
-      if (i >= n) {
-        base = -1;
-      } else if (p.paged) {
-        base = -1;
-        if (row >= 0 && row < p.table_rows) {
-          const int entry = pg >> p.chunk_shift;
-          const long phys = tab[(long)row * p.table_w + entry];
-          if (phys >= 0 && phys < p.capacity)
-            base = ((phys * p.KH + kh) * (long)p.page + ((pg - (entry << p.chunk_shift)) << 4)) * (long)D;
-        }
-      } else {
-        base = (row >= 0 && row < p.capacity) ? (((long)row * p.KH + kh) * (long)p.page + (long)pg * 16) * (long)D : -1;
-      }
-      base = (long)uniform_ptr((const char *)base);
-      const int live = base < 0 ? 0 : max(0, min(16, s_hi - pg * 16));
-      const long off = base < 0 ? 0 : (F32 ? 4 : 2) * base;
-      const int bytes = uniform(live * ROWB);
-      return ChunkRsrc{
-          __builtin_amdgcn_make_buffer_rsrc((void *)uniform_ptr(kplane + off), (short)0, bytes, kRawBufferWord3),
-          __builtin_amdgcn_make_buffer_rsrc((void *)uniform_ptr(vplane + off), (short)0, bytes, kRawBufferWord3)};
-    };
-    // Chunk i straight into LDS `stage` (direct-to-LDS loads).
-    auto issue = [&](int i, int stage) __attribute__((always_inline)) {
-      const ChunkRsrc r = chunk_rsrc(i);
-      char *dst = s_ring + (w * NB + stage) * STAGE;
-  #pragma unroll
-      for (int j = 0; j < IPP; ++j)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r.k, (lds_void *)(dst + 1024 * j), 16, dma_off[j], 0, 0,
-                                                 kStreamLoadAux);
-  #pragma unroll
-      for (int j = 0; j < IPP; ++j)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r.v, (lds_void *)(dst + PAGEB + 1024 * j), 16, dma_off[j], 0, 0,
-                                                 kStreamLoadAux);
-    };
-
-    f32x4 o[MD];
-  #pragma unroll
-    for (int md = 0; md < MD; ++md) o[md] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = kNegInf;  // running max of this lane's head (log2 domain)
-    float lsum = 0.f;       // this lane's share of the running denominator
-
-    auto consume = [&](int i, auto stage_tag) __attribute__((always_inline)) {
-      constexpr int SOFF = decltype(stage_tag)::value * STAGE;
-      const int t0 = (first + i * NW) * 16;
-      u32x4 ka[NC];
-      u32x2 va[F32 ? 1 : MD];
-      u32x4 vf[F32 && !V8 ? MD : 1];
-      u32x2 vh[V8 ? 2 * MD : 1];
-  #pragma unroll
-      for (int c = 0; c < NC; ++c) ka[c] = lds_read_b128<SOFF>(k_addr[c]);
-      if constexpr (V8) {
-  #pragma unroll
-        for (int j = 0; j < 2 * MD; ++j) vh[j] = lds_read_b64<SOFF>(v_addr[j]);
-      } else {
-  #pragma unroll
-        for (int md = 0; md < MD; ++md) {
-          if constexpr (F32) {
-            vf[md] = lds_read_b128<SOFF>(v_addr[md]);
-          } else {
-            va[md] = lds_read_tr16<SOFF>(v_addr[md]);
-          }
-        }
-      }
-      wait_lds();
-  #pragma unroll
-      for (int c = 0; c < NC; ++c) after_wait(ka[c]);
-      if constexpr (V8) {
-  #pragma unroll
-        for (int j = 0; j < 2 * MD; ++j) after_wait(vh[j]);
-      } else {
-  #pragma unroll
-        for (int md = 0; md < MD; ++md) {
-          if constexpr (F32) {
-            after_wait(vf[md]);
-          } else {
-            after_wait(va[md]);
-          }
-        }
-      }
-      // The stage is in registers now: refill it with chunk i + NB.
-      issue(i + NB, decltype(stage_tag)::value);
-
-      f32x4 s = {0.f, 0.f, 0.f, 0.f};
-      if constexpr (F32) {
-  #pragma unroll
-        for (int c = 0; c < NC; ++c)
-  #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            s = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(ka[c][q]), __uint_as_float(qa[c][q]), s, 0, 0,
-                                                     0);
-      } else {
-  #pragma unroll
-        for (int c = 0; c < NC; ++c) s = mfma16x16x32<DT>(ka[c], qa[c], s);
-      }
-
-      // logits of tokens t0 + 4kg + i for head n16
-      float x[4];
-      float mx = kNegInf;
-      float rb[4] = {0.f, 0.f, 0.f, 0.f};
-      if (p.rel) {  // workgroup-uniform: no per-lane branch in the common path
-  #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int t = t0 + 4 * kg + e;
-          const long dist = pos64 - t > 0 ? pos64 - t : 0;
-          rb[e] = p.rel[((long)kh * p.G + gofs + (col_on ? n16 : 0)) * p.rel_buckets +
-                        rel_bucket((int)dist, p.rel_buckets, p.rel_denom)] * kLog2e;
-        }
-      }
-  #pragma unroll
+    // logits of tokens t0 + 4kg + i for head n16
+    float x[4];
+    float mx = kNegInf;
+    float rb[4] = {0.f, 0.f, 0.f, 0.f};
+    if (p.rel) {  // workgroup-uniform: no per-lane branch in the common path
+#pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int t = t0 + 4 * kg + e;
-        const float v = s[e] * p.scale_log2 + slope * (float)t + rb[e];
-        x[e] = (t >= s_lo && t < s_hi) ? v : kNegInf;
-        mx = fmaxf(mx, x[e]);
+        const long dist = pos64 - t > 0 ? pos64 - t : 0;
+        rb[e] = p.rel[((long)kh * p.G + gofs + (col_on ? n16 : 0)) * p.rel_buckets +
+                      rel_bucket((int)dist, p.rel_buckets, p.rel_denom)] * kLog2e;
       }
-      mx = xor32_max(xor16_max(mx));
-      const bool up = mx > m_run + kStreamSlack;
-      if (__builtin_amdgcn_ballot_w64(up)) {
-        const float mn = up ? mx : m_run;
-        const float alpha = up ? (m_run == kNegInf ? 0.f : fast_exp2(m_run - mn)) : 1.f;
-        m_run = mn;
-        lsum *= alpha;
-  #pragma unroll
-        for (int md = 0; md < MD; ++md) o[md] *= alpha;
-      }
-      const float mu = m_run == kNegInf ? 0.f : m_run;
-      float pr[4];
-  #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        pr[e] = fast_exp2(x[e] - mu);
-        lsum += pr[e];
-      }
-      if constexpr (F32) {
-        // P^T stays fp32: key 4kg + e is k-index kg of the e-th MFMA of a tile.
-        if (t0 < s_lo) {   // expired keys' V must not reach the MFMA (0 * NaN)
-  #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (t0 + 4 * kg + e < s_lo) {
-              if constexpr (V8) {
-  #pragma unroll
-                for (int q = 0; q < MD / 2; ++q) vh[e * (MD / 2) + q] = u32x2{0, 0};
-              } else {
-  #pragma unroll
-                for (int q = 0; q < MD / 4; ++q) vf[e * (MD / 4) + q] = u32x4{0, 0, 0, 0};
-              }
-            }
-        }
-  #pragma unroll
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = t0 + 4 * kg + e;
+      const float v = s[e] * p.scale_log2 + slope * (float)t + rb[e];
+      x[e] = (t >= s_lo && t < s_hi) ? v : kNegInf;
+      mx = fmaxf(mx, x[e]);
+    }
+    mx = xor32_max(xor16_max(mx));
+    const bool up = mx > m_run + kStreamSlack;
+    if (__builtin_amdgcn_ballot_w64(up)) {
+      const float mn = up ? mx : m_run;
+      const float alpha = up ? (m_run == kNegInf ? 0.f : fast_exp2(m_run - mn)) : 1.f;
+      m_run = mn;
+      lsum *= alpha;
+#pragma unroll
+      for (int md = 0; md < MD; ++md) o[md] *= alpha;
+    }
+    const float mu = m_run == kNegInf ? 0.f : m_run;
+    float pr[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      pr[e] = fast_exp2(x[e] - mu);
+      lsum += pr[e];
+    }
+    if constexpr (F32) {
+      // P^T stays fp32: key 4kg + e is k-index kg of the e-th MFMA of a tile.
+      if (t0 < s_lo) {   // expired keys' V must not reach the MFMA (0 * NaN)
+#pragma unroll
         for (int e = 0; e < 4; ++e)
-  #pragma unroll
-          for (int md = 0; md < MD; ++md)
-            o[md] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                __uint_as_float(V8 ? vh[e * (MD / 2) + md / 2][md % 2] : vf[V8 ? 0 : e * (MD / 4) + md / 4][md % 4]),
-                pr[e], o[md], 0, 0, 0);
-      } else {
-        // P^T in two 16-bit parts (high, and the residual): the P.V product
-        // then carries the fp32 probabilities to ~2^-17, as the reference's fp32
-        // weighted sum does, instead of the 2^-9 of one bf16 rounding.
-        const u32x2 pb = {pack_pair<DT>(pr[0], pr[1]), pack_pair<DT>(pr[2], pr[3])};
-        u32x2 pl;
-        {
-          float r[4];
-  #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const unsigned wd = pb[e >> 1];
-            const unsigned short hb = (unsigned short)((e & 1) ? (wd >> 16) : (wd & 0xffffu));
-            r[e] = pr[e] - (DT == DD_BF16 ? __uint_as_float((unsigned)hb << 16) : half_bits_to_float(hb));
+          if (t0 + 4 * kg + e < s_lo) {
+            if constexpr (V8) {
+#pragma unroll
+              for (int q = 0; q < MD / 2; ++q) vh[e * (MD / 2) + q] = u32x2{0, 0};
+            } else {
+#pragma unroll
+              for (int q = 0; q < MD / 4; ++q) vf[e * (MD / 4) + q] = u32x4{0, 0, 0, 0};
+            }
           }
-          pl = u32x2{pack_pair<DT>(r[0], r[1]), pack_pair<DT>(r[2], r[3])};
-        }
-
-        // Rows before the window start inside this chunk hold expired keys:
-        // their V must not reach the MFMA (0 * NaN).
-        if (t0 < s_lo) {
-          const int r0 = 4 * kg;
-  #pragma unroll
-          for (int md = 0; md < MD; ++md) {
-            unsigned lo = va[md][0], hi = va[md][1];
-            if (t0 + r0 + 0 < s_lo) lo &= 0xffff0000u;
-            if (t0 + r0 + 1 < s_lo) lo &= 0x0000ffffu;
-            if (t0 + r0 + 2 < s_lo) hi &= 0xffff0000u;
-            if (t0 + r0 + 3 < s_lo) hi &= 0x0000ffffu;
-            va[md] = u32x2{lo, hi};
-          }
-        }
-  #pragma unroll
-        for (int md = 0; md < MD; ++md) o[md] = mfma16x16x16<DT>(va[md], pl, mfma16x16x16<DT>(va[md], pb, o[md]));
       }
-    };
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int md = 0; md < MD; ++md)
+          o[md] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+              __uint_as_float(V8 ? vh[e * (MD / 2) + md / 2][md % 2] : vf[V8 ? 0 : e * (MD / 4) + md / 4][md % 4]),
+              pr[e], o[md], 0, 0, 0);
+    } else {
+      // P^T in two 16-bit parts (high, and the residual): the P.V product
+      // then carries the fp32 probabilities to ~2^-17, as the reference's fp32
+      // weighted sum does, instead of the 2^-9 of one bf16 rounding.
+      const u32x2 pb = {pack_pair<DT>(pr[0], pr[1]), pack_pair<DT>(pr[2], pr[3])};
+      u32x2 pl;
+      {
+        float r[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const unsigned wd = pb[e >> 1];
+          const unsigned short hb = (unsigned short)((e & 1) ? (wd >> 16) : (wd & 0xffffu));
+          r[e] = pr[e] - (DT == DD_BF16 ? __uint_as_float((unsigned)hb << 16) : half_bits_to_float(hb));
+        }
+        pl = u32x2{pack_pair<DT>(r[0], r[1]), pack_pair<DT>(r[2], r[3])};
+      }
 
-    // Prologue: NB chunks in flight, then the query operand (loaded before
-    // them) is made visibly complete, so the loop carries no pending load the
-    // compiler would wait for.
-  #pragma unroll
-    for (int u = 0; u < NB; ++u) issue(u, u);
-  #pragma unroll
-    for (int c = 0; c < NC; ++c) after_wait(qa[c]);
-    after_wait(slope);
-    // Chunk i: NB - 1 younger chunks (2 IPP loads each) stay in flight.  Full
-    // groups of NB chunks run without guards and the last n % NB after the
-    // loop, so that the loop body has one path and the accumulators keep
-    // their registers across iterations.
-    auto step = [&](int i, auto u_tag) __attribute__((always_inline)) {
-      wait_vm<2 * IPP * (NB - 1)>();
-      consume(i, u_tag);
-    };
-    int i0 = 0;
-    for (; i0 + NB <= n; i0 += NB)
-      static_for<NB>([&](auto u) __attribute__((always_inline)) { step(i0 + decltype(u)::value, u); });
-    static_for<NB - 1>([&](auto u) __attribute__((always_inline)) {
-      if (i0 + decltype(u)::value < n) step(i0 + decltype(u)::value, u);
-    });
-    wait_vm<0>();  // the trailing (empty) loads, before the ring is reused
-
-    stream_epilogue<DT, D, NW>(p, s_ml, (float *)s_ring, o, m_run, lsum, w, lane, b, head0, G, split);
+      // Rows before the window start inside this chunk hold expired keys:
+      // their V must not reach the MFMA (0 * NaN).
+      if (t0 < s_lo) {
+        const int r0 = 4 * kg;
+#pragma unroll
+        for (int md = 0; md < MD; ++md) {
+          unsigned lo = va[md][0], hi = va[md][1];
+          if (t0 + r0 + 0 < s_lo) lo &= 0xffff0000u;
+          if (t0 + r0 + 1 < s_lo) lo &= 0x0000ffffu;
+          if (t0 + r0 + 2 < s_lo) hi &= 0xffff0000u;
+          if (t0 + r0 + 3 < s_lo) hi &= 0x0000ffffu;
+          va[md] = u32x2{lo, hi};
+        }
+      }
+#pragma unroll
+      for (int md = 0; md < MD; ++md) o[md] = mfma16x16x16<DT>(va[md], pl, mfma16x16x16<DT>(va[md], pb, o[md]));
+    }
   };
-  // Without p.work a workgroup runs unit blockIdx.x.  With it (dynamic
-  // schedule), p.resident workgroups start with units 0 .. resident-1 and
-  // then take the next unit from the work counter, in the static order (full
-  // splits first), so that the XCDs and CUs that run ahead take more of the
-  // tail.  The ticket of the next unit is fetched at the start of the
-  // current one and handed to every wave through LDS (double-buffered: a
-  // fast wave may write the next slot while a slow one still reads this).
-  __shared__ int s_next[2];
-  const int total = p.B * p.KH * p.gsub * p.splits;
-  int wg = blockIdx.x;
-  for (int it = 0;; ++it) {
-    int ticket = 0;
-    if (p.work && threadIdx.x == 0) ticket = atomicAdd(p.work, 1);
-    unit(wg);
-    if (!p.work) break;
-    if (threadIdx.x == 0) s_next[it & 1] = p.resident + ticket;
-    __syncthreads();   // s_next, and every wave is done with the ring
-    wg = s_next[it & 1];
-    if (wg >= total) break;
-  }
+
+  // Prologue: NB chunks in flight, then the query operand (loaded before
+  // them) is made visibly complete, so the loop carries no pending load the
+  // compiler would wait for.
+#pragma unroll
+  for (int u = 0; u < NB; ++u) issue(u, u);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) after_wait(qa[c]);
+  after_wait(slope);
+  // Chunk i: NB - 1 younger chunks (2 IPP loads each) stay in flight.  Full
+  // groups of NB chunks run without guards and the last n % NB after the
+  // loop, so that the loop body has one path and the accumulators keep
+  // their registers across iterations.
+  auto step = [&](int i, auto u_tag) __attribute__((always_inline)) {
+    wait_vm<2 * IPP * (NB - 1)>();
+    consume(i, u_tag);
+  };
+  int i0 = 0;
+  for (; i0 + NB <= n; i0 += NB)
+    static_for<NB>([&](auto u) __attribute__((always_inline)) { step(i0 + decltype(u)::value, u); });
+  static_for<NB - 1>([&](auto u) __attribute__((always_inline)) {
+    if (i0 + decltype(u)::value < n) step(i0 + decltype(u)::value, u);
+  });
+  wait_vm<0>();  // the trailing (empty) loads, before the ring is reused
+
+  stream_epilogue<DT, D, NW>(p, s_ml, (float *)s_ring, o, m_run, lsum, w, lane, b, head0, G, split);
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
-// Workgroups of `kernel` (block size `threads`) that fit on the current
-// device at once: the grid of the dynamic schedule.  0 if unknown.
-inline int resident_groups(const void *kernel, int threads) {
-  int dev = 0, cus = 0, per_cu = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess) return 0;
-  return cus * per_cu;
-}
-
 template <int DT, int D, int NB, int NW>
-int launch_stream(const DecodeParams &p_in, hipStream_t stream, int phase) {
-  DecodeParams p = p_in;
-  long grid = (long)p.B * p.KH * p.gsub * p.splits;
+int launch_stream(const DecodeParams &p, hipStream_t stream, int phase) {
+  const long grid = (long)p.B * p.KH * p.gsub * p.splits;
   if (grid <= 0) return DD_OK;
   if (grid > 0x7fffffffL) return DD_EINVAL;
-  if (p.work && p.splits > 1) {
-    // the merge kernel that resets the counter runs only when splits > 1
-    static thread_local int resident[64] = {};
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    int &r = resident[dev & 63];
-    if (!r) r = resident_groups((const void *)stream_kernel<DT, D, NB, NW>, 64 * NW);
-    p.resident = r;
-    if (r > 0 && r < grid) grid = r;
-  }
-  if (!(p.splits > 1 && p.resident > 0 && p.resident < (long)p.B * p.KH * p.gsub * p.splits)) p.work = nullptr;
   if (phase & 1) {
     hipLaunchKernelGGL((stream_kernel<DT, D, NB, NW>), dim3((unsigned)grid), dim3(64 * NW), 0, stream, p);
     DD_LAUNCH_CHECK();

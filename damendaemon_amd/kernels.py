@@ -67,41 +67,15 @@ def attention(query, cache_k, cache_v, positions, slots=None, window=0, scale=No
                     k_scale=k_scale, v_scale=v_scale))
             return out
     return prepare_attention(query, cache_k, cache_v, positions, slots, window, scale, alibi, page_table,
-                             relative_bias, relative_max_distance, sinks, k_scale=k_scale, v_scale=v_scale,
-                             work=stream_work_counter(query.device)).run()
-
-
-_WORK_COUNTERS = {}
-# tuning switch: DAMENDAEMON_AMD_STATIC_DECODE=1 runs the split kernel with one
-# unit per workgroup (no work counter)
-_STATIC_SCHEDULE = os.environ.get('DAMENDAEMON_AMD_STATIC_DECODE') == '1'
-
-
-def stream_work_counter(device):
-    """The split kernel's work counter for launches on the current stream of
-    ``device`` (one int32, zero between calls; launches on one stream never
-    overlap, so they can share it).  None while that stream is capturing a
-    graph and has no counter yet: allocating one there would put it in the
-    graph's memory pool."""
-    stream = torch.cuda.current_stream(device)
-    key = (torch.device(device).index, stream.cuda_stream)
-    counter = _WORK_COUNTERS.get(key)
-    if counter is None:
-        if torch.cuda.is_current_stream_capturing():
-            return None
-        counter = _WORK_COUNTERS[key] = torch.zeros(1, dtype=torch.int32, device=device)
-    return counter
+                             relative_bias, relative_max_distance, sinks, k_scale=k_scale, v_scale=v_scale).run()
 
 
 def prepare_attention(query, cache_k, cache_v, positions, slots=None, window=0, scale=None, alibi=None,
                       page_table=None, relative_bias=None, relative_max_distance=128, sinks=None,
-                      *, k_scale=None, v_scale=None, out=None, work=None):
+                      *, k_scale=None, v_scale=None, out=None):
     """Validate a decode call once and return its ``DecodeLaunch``.
 
     ``out`` (optional) is a preallocated (B, H, 1, D) contiguous output.
-    ``work`` (optional) is the split kernel's work counter, one int32 that
-    is zero (``stream_work_counter`` gives the current stream's); by default
-    the launch allocates its own.
 
     Arguments and errors are those of ``attention`` (damendaemon/kernels.py:213-229).
     """
@@ -152,7 +126,7 @@ def prepare_attention(query, cache_k, cache_v, positions, slots=None, window=0, 
     splits, split_tokens = _splits(context, batch * kv_heads)
     return DecodeLaunch(query, cache_k, cache_v, positions, slots, page_table, kv_heads, page_size, capacity,
                         group, k_scale, v_scale, window, scale, alibi, relative_bias, buckets,
-                        relative_max_distance, sinks, splits, split_tokens, out, work)
+                        relative_max_distance, sinks, splits, split_tokens, out)
 
 
 class DecodeLaunch:
@@ -167,7 +141,7 @@ class DecodeLaunch:
 
     def __init__(self, query, cache_k, cache_v, positions, slots, page_table, kv_heads, page_size, capacity,
                  group, k_scale, v_scale, window, scale, alibi, relative_bias, buckets, relative_max_distance,
-                 sinks, splits, split_tokens, out=None, work=None):
+                 sinks, splits, split_tokens, out=None):
         batch, heads, _, dim = query.shape
         if out is not None and (out.shape != query.shape or out.dtype != query.dtype or not out.is_contiguous()):
             raise ValueError('out must be a contiguous tensor shaped and typed like the query')
@@ -175,12 +149,8 @@ class DecodeLaunch:
         if splits > 1:
             self.partial = torch.empty((batch * heads, splits, dim), device=query.device, dtype=torch.float32)
             self.lse = torch.empty((batch * heads, splits), device=query.device, dtype=torch.float32)
-            if work is not None and (work.dtype != torch.int32 or work.device != query.device or work.numel() < 1):
-                raise ValueError('work must be one int32 on the query device')
-            # the split kernel's work counter: zero now, left at zero by every run
-            self.work = work if work is not None else torch.zeros(1, dtype=torch.int32, device=query.device)
         else:
-            self.partial = self.lse = self.work = None
+            self.partial = self.lse = None
         self.splits, self.split_tokens = splits, split_tokens
         # keep every tensor argument alive as long as the launch object
         self._keep = (query, cache_k, cache_v, positions, slots, page_table, k_scale, v_scale, alibi,
@@ -195,8 +165,7 @@ class DecodeLaunch:
             float(dim ** -.5 if scale is None else scale),
             ptr(alibi), ptr(relative_bias), buckets,
             math.log(relative_max_distance / (buckets // 2)) if buckets else 1.0,
-            ptr(sinks), ptr(self.out), ptr(self.partial), ptr(self.lse), splits, split_tokens,
-            None if _STATIC_SCHEDULE else ptr(self.work))
+            ptr(sinks), ptr(self.out), ptr(self.partial), ptr(self.lse), splits, split_tokens)
 
     def _call(self, name):
         call(name, *self._args, ctypes.c_void_p(torch.cuda.current_stream(self._device).cuda_stream))

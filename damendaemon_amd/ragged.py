@@ -184,7 +184,7 @@ def ragged_attention(query, cache_k, cache_v, packed, page_table, window=0, scal
         rows = slice(t_decode, T)
         kernels.prepare_attention(q[rows].unsqueeze(2), cache_k, cache_v, packed.positions[rows],
                                   packed.slot_ids[rows], window=window, scale=scale, page_table=page_table,
-                                  out=out[rows].unsqueeze(2), work=kernels.stream_work_counter(q.device)).run()
+                                  out=out[rows].unsqueeze(2)).run()
 
     if first_decode > 0 and first_decode < n:
         # The decode rows (HBM-bound) run on a side stream beside the prefill

@@ -83,11 +83,6 @@ int dd_decode_splits(int max_context, int batch_kv, int *split_tokens);
  *   partial    fp32 (batch*heads, splits, dim)  scratch (unused if splits==1)
  *   lse        fp32 (batch*heads, splits)       scratch (unused if splits==1)
  *   splits, split_tokens  from dd_decode_splits()
- *   work       NULL, or one int32 that is 0 before the first call and that
- *              every call leaves at 0: the split kernel's work counter
- *              (workgroups take units from it, so that the CUs and XCDs
- *              that run ahead take more of the tail); calls that share one
- *              counter must not overlap
  */
 int dd_decode_attention(const void *q, int q_dtype, const void *k,
                         const void *v, int kv_dtype, const void *k_scale,
@@ -100,7 +95,7 @@ int dd_decode_attention(const void *q, int q_dtype, const void *k,
                         const float *alibi, const float *rel_bias,
                         int rel_buckets, float rel_denom, const float *sinks,
                         void *out, float *partial, float *lse, int splits,
-                        int split_tokens, int32_t *work, void *stream);
+                        int split_tokens, void *stream);
 
 /*
  * The two launches of dd_decode_attention, callable one at a time with the
@@ -120,7 +115,7 @@ int dd_decode_partials(const void *q, int q_dtype, const void *k,
                        float scale, const float *alibi, const float *rel_bias,
                        int rel_buckets, float rel_denom, const float *sinks,
                        void *out, float *partial, float *lse, int splits,
-                       int split_tokens, int32_t *work, void *stream);
+                       int split_tokens, void *stream);
 int dd_decode_merge(const void *q, int q_dtype, const void *k, const void *v,
                     int kv_dtype, const void *k_scale, const void *v_scale,
                     int group, const int64_t *positions, const int64_t *slots,
@@ -130,7 +125,7 @@ int dd_decode_merge(const void *q, int q_dtype, const void *k, const void *v,
                     float scale, const float *alibi, const float *rel_bias,
                     int rel_buckets, float rel_denom, const float *sinks,
                     void *out, float *partial, float *lse, int splits,
-                    int split_tokens, int32_t *work, void *stream);
+                    int split_tokens, void *stream);
 
 /*
  * dd_decode_attention without the partial / lse arguments, for callers that

@@ -22,7 +22,7 @@ DEV = 'cuda'
 def static_call(launch, out):
     """The launch's dd_decode_attention arguments, minus partial/lse, into `out`."""
     args = list(launch._args)
-    args = args[:-6] + [_native.ptr(out)] + args[-3:-1]
+    args = args[:-5] + [_native.ptr(out)] + args[-2:]
     stream = ctypes.c_void_p(torch.cuda.current_stream(out.device).cuda_stream)
     _native.call('dd_decode_attention_static', *args, stream)
 
@@ -69,7 +69,7 @@ def test_static_rejects_oversized_batch():
                                        case['slots'], page_table=case['page_table'])
     args = list(launch._args)
     args[13] = 70000   # batch far beyond the static array (rows are never read: the call is refused first)
-    args = args[:-6] + [_native.ptr(launch.out)] + args[-3:-1]
+    args = args[:-5] + [_native.ptr(launch.out)] + args[-2:]
     lib = _native.library()
     code = lib.dd_decode_attention_static(*args, ctypes.c_void_p(0))
     assert code == 4  # DD_ESCRATCH
