@@ -268,7 +268,7 @@ def _scaled_v_case(lengths, starts, heads, kvh, dim, seed, magnitude):
     return case, q, slots
 
 
-@pytest.mark.parametrize('dim,heads,kvh', [(128, 16, 4), (64, 8, 2), (128, 130, 1), (96, 16, 4)])
+@pytest.mark.parametrize('dim,heads,kvh', [(128, 16, 4), (64, 8, 2), (128, 130, 1), (96, 16, 4), (256, 16, 2)])
 @pytest.mark.parametrize('spread', ['rows', 1e-6, 1e-5, 3e-3, 2e5, 1e6])
 def test_prefill_bf16_value_range(dim, heads, kvh, spread):
     """bf16 V over the whole bf16 range that matters: per-row magnitudes
