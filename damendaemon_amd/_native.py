@@ -47,7 +47,7 @@ SIGNATURES['dd_prefill_attention'] = [_p, _p, _p, _i, _p, _p, _p, _i, _i, _i, _p
                                       _f, _p, _i, _p, _p, _p]
 SIGNATURES['dd_prefill_flag_count'] = [_i, _i, _i, _i, _i, _i]
 SIGNATURES['dd_prefill_attention_phase'] = SIGNATURES['dd_prefill_attention'][:-1] + [_i, _p]
-SIGNATURES['dd_prefill_plan'] = [_p, _p, _p, _i, _i, _i, _i, _i, _p, _i]
+SIGNATURES['dd_prefill_plan'] = [_p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _i]
 SIGNATURES['dd_prefill_geometry'] = [_i, ctypes.POINTER(_i), ctypes.POINTER(_i)]
 SIGNATURES['dd_prefill_indices'] = [_i64, _i, _i, _i64, _i64, _p, _p]
 SIGNATURES['dd_ring_decode_indices'] = [_p, _i64, _i, _i, _i, _p, _p]

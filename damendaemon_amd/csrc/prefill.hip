@@ -40,6 +40,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <functional>
 #include <type_traits>
 #include <vector>
 
@@ -651,7 +652,8 @@ extern "C" int dd_prefill_geometry(int dim, int *columns, int *keys_per_tile) {
 // of XCD x (item -1 pads the shorter XCD lists).  An entry is kPlanInts
 // ints: the item, then its segment's token offset, length, start and slot.
 extern "C" int dd_prefill_plan(const int64_t *lengths, const int64_t *starts, const int64_t *slots, int n,
-                               int heads, int kv_heads, int dim, int window, int32_t *plan, int capacity) {
+                               int heads, int kv_heads, int dim, int window, int workgroups, int32_t *plan,
+                               int capacity) {
   if (!lengths || !starts || !slots || n < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || capacity < 0)
     return -DD_EINVAL;
   Geometry g;
@@ -705,20 +707,49 @@ extern "C" int dd_prefill_plan(const int64_t *lengths, const int64_t *starts, co
     std::stable_sort(l.begin(), l.end());
     longest = std::max(longest, l.size());
   }
-  const long need = (long)kXcds * (long)longest;
+  // Workgroup b runs on XCD b % 8.  Without a workgroup count: one item per
+  // workgroup, item j of XCD x in workgroup 8 j + x (the hardware hands the
+  // next workgroup to whichever CU frees first).  With one (at most one per
+  // CU, so that all of them run at once): the items of XCD x go, longest
+  // first, each to the least-loaded of that XCD's workgroups, which run them
+  // in that order -- round r of workgroup b is entry r * G + b.
+  long grid = (long)kXcds * (long)longest, rounds = 1;
+  std::vector<std::vector<int>> per_wg;  // items of each workgroup (persistent form)
+  if (workgroups >= kXcds && (long)workgroups / kXcds < (long)longest) {
+    grid = (workgroups / kXcds) * kXcds;
+    const long per_xcd = grid / kXcds;
+    per_wg.assign(grid, {});
+    for (int x = 0; x < kXcds; ++x) {
+      std::vector<std::pair<long, long>> bins;  // (load, wg)
+      for (long i = 0; i < per_xcd; ++i) bins.push_back({0, kXcds * i + x});
+      std::make_heap(bins.begin(), bins.end(), std::greater<>());
+      for (const auto &cw : lists[x]) {
+        std::pop_heap(bins.begin(), bins.end(), std::greater<>());
+        bins.back().first -= cw.first;   // cw.first is -cost
+        per_wg[bins.back().second].push_back(cw.second);
+        std::push_heap(bins.begin(), bins.end(), std::greater<>());
+      }
+    }
+    rounds = 0;
+    for (const auto &l : per_wg) rounds = std::max<long>(rounds, (long)l.size());
+  }
+  const long need = grid * rounds;
   if (need > 0x7fffffffL) return -DD_EUNSUPPORTED;
   if (!plan || capacity < need) return (int)need;
-  for (size_t j = 0; j < longest; ++j)
-    for (int x = 0; x < kXcds; ++x) {
-      int32_t *e = plan + (long)kPlanInts * (kXcds * j + x);
+  auto item_of = [&](long r, long b) -> int {
+    if (!per_wg.empty()) return r < (long)per_wg[b].size() ? per_wg[b][r] : -1;
+    const long j = b / kXcds, x = b % kXcds;   // one round
+    return j < (long)lists[x].size() ? lists[x][j].second : -1;
+  };
+  for (long r = 0; r < rounds; ++r)
+    for (long b = 0; b < grid; ++b) {
+      int32_t *e = plan + (long)kPlanInts * (r * grid + b);
       for (int k = 0; k < kPlanInts; ++k) e[k] = 0;
-      if (j >= lists[x].size()) {
-        e[0] = -1;
-        continue;
-      }
-      const int item = lists[x][j].second;
-      const int seg = (int)(item / max_tiles) / kv_heads;
+      e[5] = (int32_t)rounds;
+      const int item = item_of(r, b);
       e[0] = item;
+      if (item < 0) continue;
+      const int seg = (int)(item / max_tiles) / kv_heads;
       e[1] = (int32_t)tok0[seg];
       e[2] = (int32_t)lengths[seg];
       e[3] = (int32_t)starts[seg];

@@ -45,15 +45,21 @@ struct PrefillParams {
 // (segment seg, KV head).  A plan entry (dd_prefill_plan) carries the item
 // and its segment's token offset, length, start and slot, so that a
 // workgroup reads them with one load instead of a chain of two.
-constexpr int kPlanInts = DD_PREFILL_PLAN_INTS;   // item, tok0, len, start, slot, 3 unused
+constexpr int kPlanInts = DD_PREFILL_PLAN_INTS;   // item, tok0, len, start, slot, rounds, 2 unused
 struct PrefillItem {
   int grp, qt, seg, len, start;
   long tok0, slot;
 };
-// false: the workgroup has nothing to do
-DD_DEV bool prefill_item(const PrefillParams &p, PrefillItem &it) {
+// Work items per workgroup under a plan: the plan holds `rounds` entries per
+// workgroup, round-major (entry round * gridDim.x + blockIdx.x); every entry
+// stores the count (field 5).  1 without a plan.
+DD_DEV int prefill_rounds(const PrefillParams &p) {
+  return p.plan ? p.plan[(long)kPlanInts * blockIdx.x + 5] : 1;
+}
+// Item of round `round` of this workgroup; false: nothing to do
+DD_DEV bool prefill_item(const PrefillParams &p, PrefillItem &it, int round = 0) {
   if (p.plan) {
-    const int32_t *e = p.plan + (long)kPlanInts * blockIdx.x;
+    const int32_t *e = p.plan + (long)kPlanInts * ((long)round * gridDim.x + blockIdx.x);
     const int item = e[0];
     if (item < 0) return false;
     it.grp = item / p.max_tiles;

@@ -178,9 +178,19 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   const int l32 = lane & 31;
   const int h2 = lane >> 5;
 
-  PrefillItem it;
-  if (!prefill_item(p, it)) return;
   __shared__ int s_flag;   // some column of this item needs the exact re-run
+  // A workgroup runs the plan's items for it one after another (one
+  // workgroup per CU: no dispatch gap between them, and the next item's
+  // plan entry is known before the current one ends).
+  const int rounds = prefill_rounds(p);
+  for (int round = 0; round < rounds; ++round) {
+  PrefillItem it;
+  if (!prefill_item(p, it, round)) break;
+  if (round > 0) {
+    // every wave has read its previous output tile out of the V ring
+    lgkm_drain();
+    barrier();
+  }
   const int grp = it.grp, qt = it.qt, seg = it.seg;
   const int kh = grp - seg * p.KH;
   const long tok0 = it.tok0;
@@ -188,7 +198,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   const int G = p.G;
   const int rows = COLS / G;
   const int r0 = qt * rows;
-  if (r0 >= len) return;
+  if (r0 >= len) continue;
   const int start = it.start;
   const int context = start + len;
   const long slot = it.slot;
@@ -647,6 +657,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
       const u32x4 x = *(const u32x4 *)(otile + c * ORS + 16 * k);
       *(u32x4 *)(dst + ((tok0 + r0 + cq) * p.H + (long)kh * G + cg) * DR + 8 * k) = x;
     }
+  }
   }
 }
 

@@ -11,6 +11,7 @@ pages directly; nothing is gathered.
 """
 import ctypes
 import math
+import os
 
 import numpy as np
 import torch
@@ -42,14 +43,16 @@ def _has_mfma_geometry(dim):
     return _native.library().dd_prefill_geometry(int(dim), ctypes.byref(cols), ctypes.byref(keys)) == 0
 
 
-def prefill_plan(lengths, starts, heads, kv_heads, dim, window=0, slots=None):
-    """Workgroup order of the prefill kernel for these segments: a host int32
-    array (entries, 8), each row (item or -1, first packed token, length,
-    start, slot, 0, 0, 0).
+def prefill_plan(lengths, starts, heads, kv_heads, dim, window=0, slots=None, workgroups=0):
+    """Schedule of the prefill kernel for these segments: a host int32 array
+    (entries, 8), each row (item or -1, first packed token, length, start,
+    slot, rounds, 0, 0); entry r * G + b is round r of workgroup b.
 
     Balances (segment, KV head, query tile) items over the XCDs, longest
     first, from the host copies of the segment lengths, starts and slots
-    (slots default to 0 .. n-1).
+    (slots default to 0 .. n-1).  ``workgroups`` > 0 (the number of CUs)
+    gives each of at most that many workgroups a list of items to run in
+    turn; 0 gives one item per workgroup.
     """
     lengths = np.ascontiguousarray(lengths, dtype=np.int64)
     starts = np.ascontiguousarray(starts, dtype=np.int64)
@@ -58,7 +61,8 @@ def prefill_plan(lengths, starts, heads, kv_heads, dim, window=0, slots=None):
         raise ValueError('lengths, starts and slots must be matching 1-D sequences')
     lib = _native.library()
     args = (lengths.ctypes.data_as(ctypes.c_void_p), starts.ctypes.data_as(ctypes.c_void_p),
-            slots.ctypes.data_as(ctypes.c_void_p), len(lengths), heads, kv_heads, dim, int(window or 0))
+            slots.ctypes.data_as(ctypes.c_void_p), len(lengths), heads, kv_heads, dim, int(window or 0),
+            int(workgroups))
     need = lib.dd_prefill_plan(*args, None, 0)
     if need < 0:
         raise _native.NativeError(f'dd_prefill_plan failed: {lib.dd_error_string(-need).decode()} ({-need})')
@@ -113,11 +117,11 @@ def prepare_prefill(query, cache_k, cache_v, packed, page_table, window=0, scale
         # the MFMA kernel's XCD-balanced workgroup order (the fp32 / other-D
         # kernel takes none)
         plan = prefill_plan(packed.lengths[a:b], packed.starts[a:b], H, cache_k.shape[1], D, window,
-                            packed.slots[a:b])
+                            packed.slots[a:b], _persistent_workgroups(q.device, D))
         if len(plan) == 0:
             return PrefillLaunch(out, None)
         plan_dev = _native.upload(torch.from_numpy(plan), q.device)
-        plan_len = len(plan)
+        plan_len = len(plan) // int(plan[0, 5])     # workgroups
     n_flags = prefill_flag_count(b - a, max_len, H, cache_k.shape[1], D, q.dtype)
     # per-item exactness flags of the bf16 kernel (written by the kernel itself)
     if flags is not None:
@@ -154,6 +158,24 @@ class PrefillLaunch:
             call('dd_prefill_attention_phase', *self._args, int(which),
                  ctypes.c_void_p(torch.cuda.current_stream(self.out.device).cuda_stream))
         return self.out
+
+
+_CU_COUNT = {}
+
+
+def _persistent_workgroups(device, dim):
+    """Workgroup count for a persistent prefill schedule: one per CU for the
+    kernel that runs its items in turn (head sizes up to 128), else 0."""
+    if dim > 128:
+        return 0
+    forced = os.environ.get('DAMENDAEMON_AMD_PREFILL_WORKGROUPS')   # tuning: 0 = one item per workgroup
+    if forced is not None:
+        return int(forced)
+    index = torch.device(device).index
+    index = torch.cuda.current_device() if index is None else index
+    if index not in _CU_COUNT:
+        _CU_COUNT[index] = torch.cuda.get_device_properties(index).multi_processor_count
+    return _CU_COUNT[index]
 
 
 def prefill_flag_count(segments, max_len, heads, kv_heads, dim, dtype):

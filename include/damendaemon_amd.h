@@ -256,8 +256,8 @@ int dd_rope_batch(const void *qkv, int qkv_dtype, const void *cos,
  *   scale         any finite value (non-finite: DD_EINVAL); 0 gives uniform
  *                 weights over each row's allowed keys, as SDPA does
  *   plan          NULL, or the device copy of dd_prefill_plan's output for
- *                 these same segments (plan_len entries): the workgroup
- *                 order; NULL uses a fixed XCD-aware order
+ *                 these same segments, plan_len = its workgroup count G:
+ *                 the schedule; NULL uses a fixed XCD-aware order
  *   flags         device int32 workspace of dd_prefill_flag_count(...)
  *                 entries (NULL allowed when that count is 0).  The bf16
  *                 kernel at dim 64/128 multiplies V in fp16; a work item
@@ -306,16 +306,22 @@ int dd_prefill_flag_count(int n, int max_len, int heads, int kv_heads,
  * Host-side schedule for dd_prefill_attention (no reference counterpart:
  * the reference runs one SDPA per segment, paged.py:97-111).  lengths,
  * starts and slots are HOST int64 arrays (n), the same segments as the
- * call's device metadata.  Writes the workgroup order to plan (host int32,
- * DD_PREFILL_PLAN_INTS per entry, capacity entries): each entry holds the
- * work item (-1: none) and its segment's first packed token, length, start
- * and slot.  Returns the number of entries; with plan == NULL or too small
- * a capacity it only returns that number.  Negative = -DD_E*.
+ * call's device metadata.  Writes the schedule to plan (host int32,
+ * DD_PREFILL_PLAN_INTS per entry, capacity entries): each entry holds a
+ * work item (-1: none), its segment's first packed token, length, start
+ * and slot, and the number of rounds R (the same in every entry).  Entry
+ * r * G + b is round r of workgroup b; G = (entries returned) / R is the
+ * plan_len dd_prefill_attention takes.  workgroups <= 0: one item per
+ * workgroup (R = 1); otherwise at most that many workgroups, each running
+ * its items one after another (give the number of CUs: one workgroup fits
+ * per CU).  Returns the number of entries; with plan == NULL or too small a
+ * capacity it only returns that number.  Negative = -DD_E*.
  */
 #define DD_PREFILL_PLAN_INTS 8
 int dd_prefill_plan(const int64_t *lengths, const int64_t *starts,
                     const int64_t *slots, int n, int heads, int kv_heads,
-                    int dim, int window, int32_t *plan, int capacity);
+                    int dim, int window, int workgroups, int32_t *plan,
+                    int capacity);
 
 /*
  * Tile geometry of dd_prefill_attention for head size dim: (query row,

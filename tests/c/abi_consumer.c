@@ -34,12 +34,12 @@ int main(void) {
   const int64_t lengths[3] = {512, 300, 17};
   const int64_t starts[3] = {4000, 0, 900};
   const int64_t slots[3] = {5, 2, 7};
-  const int need = dd_prefill_plan(lengths, starts, slots, 3, 32, 8, 128, 0, NULL, 0);
+  const int need = dd_prefill_plan(lengths, starts, slots, 3, 32, 8, 128, 0, 0, NULL, 0);
   CHECK(need > 0 && need % 8 == 0);
   static int32_t entries[4096 * DD_PREFILL_PLAN_INTS];
   int32_t plan[4096];
   CHECK(need <= 4096);
-  CHECK(dd_prefill_plan(lengths, starts, slots, 3, 32, 8, 128, 0, entries, need) == need);
+  CHECK(dd_prefill_plan(lengths, starts, slots, 3, 32, 8, 128, 0, 0, entries, need) == need);
   for (int i = 0; i < need; ++i) {
     const int32_t *e = entries + (long)i * DD_PREFILL_PLAN_INTS;
     plan[i] = e[0];

@@ -52,7 +52,7 @@ def test_plan_covers_every_tile_once_grouped_per_xcd_longest_first(seed):
     tok0 = np.concatenate([[0], np.cumsum(lengths)])
     for e in entries[plan >= 0]:
         seg = int(e[0]) // max_tiles // kv_heads
-        assert list(e[1:5]) == [tok0[seg], lengths[seg], starts[seg], seg] and not e[5:].any()
+        assert list(e[1:6]) == [tok0[seg], lengths[seg], starts[seg], seg, 1] and not e[6:].any()
     real = plan[plan >= 0].tolist()
     assert sorted(real) == sorted(cost)             # every item exactly once
     xcd_of_group = {}
@@ -88,3 +88,45 @@ def test_plan_rejects_bad_arguments():
     assert len(ragged.prefill_plan([], [], 8, 2, 128)) == 0
     cols, kt = ctypes.c_int(), ctypes.c_int()
     assert _native.library().dd_prefill_geometry(160, ctypes.byref(cols), ctypes.byref(kt)) != 0
+
+
+@pytest.mark.parametrize('seed', range(4))
+def test_persistent_plan_rounds(seed):
+    """With a workgroup count, each workgroup gets a list of items (round r
+    of workgroup b at entry r * G + b): every item once, each list on its
+    workgroup's XCD (b % 8, the XCD of the item's group in the one-item
+    plan), and within an XCD the loads balanced as longest-first greedy
+    assignment guarantees (max - min <= the largest item)."""
+    rng = random.Random(seed)
+    dim = rng.choice([64, 96, 128])
+    kv_heads = rng.choice([2, 8])
+    heads = kv_heads * rng.choice([1, 4])
+    n = rng.randint(4, 12)
+    lengths = [rng.choice([64, 300, 512, 1000]) for _ in range(n)]
+    starts = [rng.randint(0, 5000) for _ in range(n)]
+    flat = ragged.prefill_plan(lengths, starts, heads, kv_heads, dim, 0)
+    xcd_of_group = {}
+    cost, max_tiles = _items(lengths, starts, heads, kv_heads, dim, 0)
+    for idx, item in enumerate(flat[:, 0]):
+        if item >= 0:
+            xcd_of_group[int(item) // max_tiles] = idx % 8
+    plan = ragged.prefill_plan(lengths, starts, heads, kv_heads, dim, 0, workgroups=64)
+    rounds = int(plan[0, 5])
+    wgs = len(plan) // rounds     # fewer when every item gets a workgroup of its own
+    assert (plan[:, 5] == rounds).all() and wgs * rounds == len(plan) and wgs <= 64 and wgs % 8 == 0
+    items = plan[:, 0].reshape(rounds, wgs)
+    real = items[items >= 0].tolist()
+    assert sorted(real) == sorted(cost)
+    load = [0] * wgs
+    for b in range(wgs):
+        for r in range(rounds):
+            item = int(items[r, b])
+            if item < 0:
+                assert (items[r:, b] < 0).all()     # padding only at the end
+                break
+            assert xcd_of_group[item // max_tiles] == b % 8
+            load[b] += cost[item]
+    biggest = max(cost.values())
+    for x in range(8):
+        ls = load[x::8]
+        assert max(ls) - min(ls) <= biggest + 2 * rounds + 2   # the schedule also charges 2 per item
