@@ -47,6 +47,7 @@ namespace dd_decode {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 #ifndef DD_STREAM_NB128
@@ -913,10 +914,19 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
     qoff[c] = kI8Offset * xor32_sum(xor16_sum(qs));   // column n16's sum over the 32 dims of chunk c
   }
 
+  // NG == 1: the S^T accumulator starts at minus the query's offset sum, so
+  // the MFMAs leave q.k itself
+  float qo_all = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) qo_all += qoff[c];
+  const f32x4 s_init = {-qo_all, -qo_all, -qo_all, -qo_all};
+
   f32x4 o[MD];
 #pragma unroll
   for (int md = 0; md < MD; ++md) o[md] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = kNegInf;   // running max of logit + exponent of the V scale
+  // running max of logit + exponent of the V scale (+ kExpBias)
+  constexpr float kExpBias = NG == 1 ? 14.f : 0.f;
+  float m_run = kNegInf;
   float lsum = 0.f;        // sum of exp2(logit - m_run)
   float psum[NG];          // sums of the fp16 P^T operands (this lane's keys)
 #pragma unroll
@@ -957,32 +967,53 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
     issue(i + NB, decltype(stage_tag)::value);
 
     // scale of key 4kg + e of chunk ch, channel group g (fp16 at index e NG + g)
-    auto scale_of = [&](const u32x2 (&sc)[2][NG], int ch, int e, int g) __attribute__((always_inline)) {
+    auto scale_half = [&](const u32x2 (&sc)[2][NG], int ch, int e, int g) __attribute__((always_inline)) {
       const int idx = e * NG + g;
       const unsigned wd = sc[ch][idx >> 2][(idx >> 1) & 1];
-      return half_bits_to_float((unsigned short)((idx & 1) ? (wd >> 16) : (wd & 0xffffu)));
+      return __builtin_bit_cast(f16x2, wd)[idx & 1];
+    };
+    auto scale_of = [&](const u32x2 (&sc)[2][NG], int ch, int e, int g) __attribute__((always_inline)) {
+      return (float)scale_half(sc, ch, e, g);
+    };
+    // x * scale in one mixed-precision FMA (the fp16 scale is read in place)
+    auto times_scale = [&](float x, const u32x2 (&sc)[2][NG], int ch, int e, int g) __attribute__((always_inline)) {
+      return __builtin_fmaf(x, (float)scale_half(sc, ch, e, g), 0.f);
+    };
+    // Biased exponent E of a V scale, from its fp16 bits: a normal scale
+    // lies in [2^(E-15), 2^(E-14)), so E - 14 bounds its frexp exponent
+    // (zero and subnormal scales get the bound -14).  The 14 is left in y
+    // and the running max (kExpBias) and taken out of the offset once.
+    auto scale_exp = [&](const u32x2 (&sc)[2][NG], int ch, int e) __attribute__((always_inline)) {
+      const int idx = e * NG;
+      const unsigned wd = sc[ch][idx >> 2][(idx >> 1) & 1];
+      return (float)__builtin_amdgcn_ubfe(wd, (idx & 1) ? 26u : 10u, 5u);
     };
     // The common case -- every key of the pair inside [s_lo, s_hi), no ALiBi,
     // no relative bias -- runs a copy of the step without masks or bias terms.
     auto body = [&](auto fast_tag) __attribute__((always_inline)) {
     constexpr bool FAST = decltype(fast_tag)::value;
-    // logits x = key t0 + 16 ch + 4 kg + e for head n16; y adds the exponent
-    // of the key's largest V scale (the quantity the running max tracks)
-    float x[2][4], y[2][4], vsf[2][4];  // vsf: V scale of the key (NG == 1 only)
+    // One scale per row and every key live: the logit is kept as
+    // x = q.k * k_scale and the logit scale folded into the FMAs that use it.
+    constexpr bool FOLD = FAST && NG == 1;
+    const float xmul = FOLD ? lscale : 1.f;
+    // logits x * xmul = key t0 + 16 ch + 4 kg + e for head n16; y adds the
+    // exponent of the key's largest V scale (the quantity the running max
+    // tracks)
+    float x[2][4], y[2][4];
     bool lv[2][4];                        // key inside [s_lo, s_hi)
     float mx = kNegInf;
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
       f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
       if constexpr (NG == 1) {
-        float qo = 0.f;
+        sacc = s_init;
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          sacc = mfma16x16x32<DD_F16>(widen_i8x8_off(k8[ch][c]), qh[c], sacc);
-          qo += qoff[c];
+        for (int c = 0; c < NC; ++c) sacc = mfma16x16x32<DD_F16>(widen_i8x8_off(k8[ch][c]), qh[c], sacc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sacc[e] = times_scale(sacc[e], ks8, ch, e, 0);
+          if constexpr (!FOLD) sacc[e] *= lscale;
         }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sacc[e] = (sacc[e] - qo) * (scale_of(ks8, ch, e, 0) * lscale);
       } else {
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
@@ -1010,10 +1041,9 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
         const float v = FAST ? sacc[e] : sacc[e] + slope * (float)t + rb[e];
         // Exponent of the key's largest V scale; dead keys' scales may be
         // garbage: they enter P as 0.
-        int ex = 0;
+        float ex = 0.f;
         if constexpr (NG == 1) {
-          vsf[ch][e] = live ? scale_of(vs8, ch, e, 0) : 0.f;
-          ex = __builtin_amdgcn_frexp_expf(vsf[ch][e]);
+          ex = live ? scale_exp(vs8, ch, e) : 0.f;
         } else {
           // From the fp16 bits: scales are >= 0, so the largest bit pattern
           // is the largest scale, and a normal one with biased exponent E
@@ -1026,11 +1056,11 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
             const unsigned wd = vs8[ch][k >> 1][k & 1];
             mh = max(mh, max(wd & 0xffffu, wd >> 16));
           }
-          ex = live && mh ? (int)((mh >> 10) & 31u) - 14 : 0;
+          ex = live && mh ? (float)((int)((mh >> 10) & 31u) - 14) : 0.f;   // (kExpBias 0)
         }
         lv[ch][e] = live;
         x[ch][e] = live ? v : kNegInf;
-        y[ch][e] = live ? v + (float)ex : kNegInf;
+        y[ch][e] = live ? __builtin_fmaf(v, xmul, ex) : kNegInf;
         mx = fmaxf(mx, y[ch][e]);
       }
     }
@@ -1046,7 +1076,7 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
 #pragma unroll
       for (int md = 0; md < MD; ++md) o[md] *= alpha;
     }
-    const float mu = m_run == kNegInf ? 0.f : m_run;
+    const float mu = m_run == kNegInf ? 0.f : m_run - kExpBias;
     // p = exp2(x - mu) <= 2^(8 - exponent of the key's V scale), so every
     // p * v_scale <= 2^8 fits fp16; dead keys have p = 0.
     float pr[2][4];
@@ -1054,7 +1084,7 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
     for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        pr[ch][e] = fast_exp2(x[ch][e] - mu);
+        pr[ch][e] = fast_exp2(__builtin_fmaf(x[ch][e], xmul, -mu));
         lsum += pr[ch][e];
       }
     // P^T operand per V scale group: slot j < 4 is key 4kg + j of chunk 0,
@@ -1065,15 +1095,10 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int ch = j >> 1, e = 2 * (j & 1);
-        float s0, s1;
-        if constexpr (NG == 1) {
-          s0 = vsf[ch][e];
-          s1 = vsf[ch][e + 1];
-        } else {
-          s0 = lv[ch][e] ? scale_of(vs8, ch, e, g) : 0.f;
-          s1 = lv[ch][e + 1] ? scale_of(vs8, ch, e + 1, g) : 0.f;
-        }
-        pb[g][j] = cvt_pk_f16(pr[ch][e] * s0, pr[ch][e + 1] * s1);
+        // (a dead key's scale may be garbage; its p is 0)
+        const float p0 = lv[ch][e] ? times_scale(pr[ch][e], vs8, ch, e, g) : 0.f;
+        const float p1 = lv[ch][e + 1] ? times_scale(pr[ch][e + 1], vs8, ch, e + 1, g) : 0.f;
+        pb[g][j] = cvt_pk_f16(p0, p1);
         psum[g] = dot2_f16(pb[g][j], 0x3C003C00u, psum[g]);
       }
     }
@@ -1114,7 +1139,7 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
 #pragma unroll
   for (int md = 0; md < MD; ++md) o[md] -= psum[NG == 1 ? 0 : (16 * md) / 32];
 
-  stream_epilogue<QT, D, NW>(p, s_ml, (float *)s_ring, o, m_run, lsum, w, lane, b, head0, G, split);
+  stream_epilogue<QT, D, NW>(p, s_ml, (float *)s_ring, o, m_run - kExpBias, lsum, w, lane, b, head0, G, split);
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
