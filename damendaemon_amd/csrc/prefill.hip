@@ -79,10 +79,17 @@ namespace {
 // zeros: every chunk load goes through a buffer resource whose size covers
 // only the chunk's live rows (out-of-range buffer loads return 0).
 
-template <int DT, int D, int NQ, int KT, int NW>
+// D is the LDS layout's head size; DR <= D the real one (a multiple of 16
+// above D / 2): rows are DR elements long in memory, the layout's dims DR ..
+// D-1 are loaded as zeros (DMA lanes past DR read out of the resource's
+// range) and the MFMAs skip the k-chunks and O^T tiles that hold only them.
+template <int DT, int D, int NQ, int KT, int NW, int DR = D>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4))) void prefill_kernel(PrefillParams p) {
-  constexpr int NC = D / 32;           // k-chunks of q.k
-  constexpr int MD = D / 16;           // O^T row tiles
+  static_assert(DR % 16 == 0 && DR <= D && 2 * DR > D, "real head size");
+  constexpr int NC = D / 32;           // k-chunks of q.k (layout)
+  constexpr int NCR = (DR + 31) / 32;  // k-chunks holding real dims
+  constexpr int MD = D / 16;           // O^T row tiles (layout)
+  constexpr int MDR = DR / 16;         // O^T row tiles of real dims
   constexpr int MT = KT / 16;          // 16-key chunks per tile
   constexpr int C2 = KT / 32;          // 32-key MFMA k-steps of P.V per tile
   constexpr int COLS = 16 * NQ * NW;   // (query row, head) columns per workgroup
@@ -153,7 +160,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
   // ---- per-lane query columns and Q^T operands ----
   int qpos[NQ];
   bool colok[NQ];
-  u32x4 qb[NQ][NC];
+  u32x4 qb[NQ][NCR];
   const unsigned short *qsrc = (const unsigned short *)p.q;
 #pragma unroll
   for (int nq = 0; nq < NQ; ++nq) {
@@ -164,12 +171,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
     qpos[nq] = start + r0 + (colok[nq] ? r : 0);
     const long row = (tok0 + r0 + (colok[nq] ? r : 0)) * p.H + (long)kh * G + gh;
 #pragma unroll
-    for (int cc = 0; cc < NC; ++cc) {
-      qb[nq][cc] = colok[nq] ? *(const u32x4 *)(qsrc + row * D + 8 * g4 + 32 * cc) ^ p.q_sign : u32x4{0, 0, 0, 0};
+    for (int cc = 0; cc < NCR; ++cc) {
+      const bool live = colok[nq] && 32 * cc + 8 * g4 < DR;
+      qb[nq][cc] = live ? *(const u32x4 *)(qsrc + row * DR + 8 * g4 + 32 * cc) ^ p.q_sign : u32x4{0, 0, 0, 0};
     }
   }
 
-  f32x4 o[MD][NQ];
+  f32x4 o[MDR][NQ];
   float m_run[NQ], alpha[NQ];
   // Row sums of P on the matrix cores: an all-ones V^T operand turns every
   // accumulator row into sum_k P[k][column] (no VALU adds, no lane reduction).
@@ -183,7 +191,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
     lacc[nq] = f32x4{0.f, 0.f, 0.f, 0.f};
     alpha[nq] = 1.f;
 #pragma unroll
-    for (int md = 0; md < MD; ++md) o[md][nq] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int md = 0; md < MDR; ++md) o[md][nq] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   __syncthreads();  // s_tab
 
@@ -199,9 +207,22 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
   };
   const int my_chunk = (w * IPW) / NC;   // every K and V block this wave loads lies in it
   const unsigned k_lane = 2u * (l16 * D + 8 * g4);             // K block, + 64cc bytes
+  // (DR < D: a lane offset per block, past every resource for dims >= DR;
+  // a wave loads at most two blocks per plane then)
+  auto k_off = [&](int j) {
+    const int d0 = 32 * ((w * IPW + j) % NC) + 8 * g4;
+    return d0 < DR ? 2u * (l16 * DR + d0) : 0x80000000u;
+  };
+  const unsigned k_dma0 = DR < D ? k_off(0) : 0u, k_dma1 = DR < D && IPW > 1 ? k_off(1) : 0u;
   const int vq = lane & 31;                                     // V: read-lane pair
   const int v_key = 4 * (vq >> 3) + ((vq & 7) >> 1);           // key within the 16-key half
   const unsigned v_lane = 2u * (v_key * D + 16 * (lane >> 5) + 8 * (vq & 1));  // + 64mp bytes
+  auto v_off = [&](int j) {
+    const int d0 = 32 * ((w * IPW + j) % (MD / 2)) + 16 * (lane >> 5) + 8 * (vq & 1);
+    return d0 < DR ? 2u * (v_key * DR + d0) : 0x80000000u;
+  };
+  const unsigned v_dma0 = DR < D ? v_off(0) : 0u, v_dma1 = DR < D && IPW > 1 ? v_off(1) : 0u;
+  static_assert(DR == D || IPW <= 2, "per-block lane offsets held as two scalars");
   // Buffer resource over this wave's chunk of tile kt in `plane` (K or V
   // pages): its size is the chunk's live rows, 0 past the context or for an
   // unallocated page.  `win` is the window that starts at tile wkt.  Each
@@ -213,10 +234,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
     const int rel = (key0 >> p.page_shift) - ((wkt * KT) >> p.page_shift);
     const int phys = __builtin_amdgcn_readlane(win, rel);
     const int live = phys < 0 ? 0 : min(16, context - key0);
-    const long base = phys < 0 ? 0 : ((((long)phys * p.KH + kh) << p.page_shift) | (key0 & (p.page - 1))) * (long)D;
+    const long base = phys < 0 ? 0 : ((((long)phys * p.KH + kh) << p.page_shift) | (key0 & (p.page - 1))) * (long)DR;
     // the resource must sit in SGPRs: make its wave-uniformity explicit
     const char *addr = uniform_ptr((const char *)plane + 2 * base);
-    return __builtin_amdgcn_make_buffer_rsrc((void *)addr, (short)0, uniform(live > 0 ? live * D * 2 : 0),
+    return __builtin_amdgcn_make_buffer_rsrc((void *)addr, (short)0, uniform(live > 0 ? live * DR * 2 : 0),
                                              kBufferWord3);
   };
   auto issue_k = [&](int win, int wkt, int kt, char *buf) __attribute__((always_inline)) {
@@ -224,7 +245,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
 #pragma unroll
     for (int j = 0; j < IPW; ++j) {
       const int blk = w * IPW + j;       // K block (mt, cc)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)(buf + blk * 1024), 16, k_lane, 64 * (blk % NC), 0, 0);
+      if constexpr (DR == D)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)(buf + blk * 1024), 16, k_lane, 64 * (blk % NC), 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)(buf + blk * 1024), 16, j == 0 ? k_dma0 : k_dma1, 0, 0,
+                                                 0);
     }
   };
   auto issue_v = [&](int win, int wkt, int kt, char *buf) __attribute__((always_inline)) {
@@ -232,8 +257,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
 #pragma unroll
     for (int j = 0; j < IPW; ++j) {
       const int blk = w * IPW + j;       // V block pair (hc, mp)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)(buf + blk * 1024), 16, v_lane,
-                                               64 * (blk % (MD / 2)), 0, 0);
+      if constexpr (DR == D)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)(buf + blk * 1024), 16, v_lane,
+                                                 64 * (blk % (MD / 2)), 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)(buf + blk * 1024), 16, j == 0 ? v_dma0 : v_dma1, 0, 0,
+                                                 0);
     }
   };
   // Wait for every load of this wave except the `recent` issued last, then
@@ -260,7 +289,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
   f32x4 s[MT][NQ];
   auto compute_s = [&](const char *kt_lds) __attribute__((always_inline)) {
 #pragma unroll
-    for (int cc = 0; cc < NC; ++cc) {
+    for (int cc = 0; cc < NCR; ++cc) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const u32x4 a = *(const u32x4 *)(kt_lds + (mt * NC + cc) * 1024 + 16 * lane);
@@ -284,7 +313,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
 #pragma unroll
       for (int nq = 0; nq < NQ; ++nq) {
 #pragma unroll
-        for (int md = 0; md < MD; ++md) o[md][nq] *= alpha[nq];
+        for (int md = 0; md < MDR; ++md) o[md][nq] *= alpha[nq];
         lacc[nq] *= alpha[nq];
       }
     }
@@ -306,8 +335,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
 #pragma unroll
     for (int c2 = 0; c2 < C2; ++c2) va[c2] = vop(0, c2);
 #pragma unroll
-    for (int md = 0; md < MD; ++md) {
-      if (md + 1 < MD) {
+    for (int md = 0; md < MDR; ++md) {
+      if (md + 1 < MDR) {
 #pragma unroll
         for (int c2 = 0; c2 < C2; ++c2) vnx[c2] = vop(md + 1, c2);
       }
@@ -316,7 +345,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
 #pragma unroll
         for (int nq = 0; nq < NQ; ++nq) o[md][nq] = mfma<DT>(va[c2], pl[c2][nq], mfma<DT>(va[c2], pb[c2][nq], o[md][nq]));
       }
-      if (md + 1 < MD) {
+      if (md + 1 < MDR) {
 #pragma unroll
         for (int c2 = 0; c2 < C2; ++c2) va[c2] = vnx[c2];
       }
@@ -450,22 +479,22 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)
     const int gh = c - r * G;
     const long row = (tok0 + r0 + r) * p.H + (long)kh * G + gh;
 #pragma unroll
-    for (int md = 0; md < MD; ++md) {
+    for (int md = 0; md < MDR; ++md) {
       const u32x2 pk = {pack2<DT>(o[md][nq][0] * inv, o[md][nq][1] * inv),
                         pack2<DT>(o[md][nq][2] * inv, o[md][nq][3] * inv)};
-      *(u32x2 *)(dst + row * D + 16 * md + 4 * g4) = pk;
+      *(u32x2 *)(dst + row * DR + 16 * md + 4 * g4) = pk;
     }
   }
 }
 
-template <int DT, int D, int NQ, int KT, int NW>
+template <int DT, int D, int NQ, int KT, int NW, int DR = D>
 int launch(PrefillParams p, int max_len, int plan_len, hipStream_t s) {
   if (16 * NQ * NW / p.G < 1) return DD_EUNSUPPORTED;
   p.max_tiles = (int)dd_cdiv(max_len, (16 * NQ * NW) / p.G);
   const long grid = p.plan ? (long)plan_len : 8L * dd_cdiv((long)p.n * p.KH, 8) * p.max_tiles;
   if (grid == 0) return DD_OK;
   if (grid > 0x7fffffffL) return DD_EUNSUPPORTED;
-  hipLaunchKernelGGL((prefill_kernel<DT, D, NQ, KT, NW>), dim3((unsigned)grid), dim3(64 * NW), 0, s, p);
+  hipLaunchKernelGGL((prefill_kernel<DT, D, NQ, KT, NW, DR>), dim3((unsigned)grid), dim3(64 * NW), 0, s, p);
   DD_LAUNCH_CHECK();
   return DD_OK;
 }
@@ -483,6 +512,8 @@ constexpr Geometry kGeom256{16 * 1 * DD_PREFILL_NW, 32};
 // Head sizes prefill_pipe_kernel takes (48 in its 64 layout, 80-112 in its
 // 128 layout).
 static bool pipe_dim(int D) { return D == 48 || D == 64 || D == 80 || D == 96 || D == 112 || D == 128; }
+// Head sizes prefill_kernel takes in its 256 layout.
+static bool wide_dim(int D) { return D > 128 && D <= 256 && D % 16 == 0; }
 
 static bool geometry(int D, Geometry *g) {
   switch (D) {
@@ -492,16 +523,28 @@ static bool geometry(int D, Geometry *g) {
     case 96:
     case 112:
     case 128: *g = kGeom128; return true;
-    case 256: *g = kGeom256; return true;
-    default: return false;
+    default:
+      if (wide_dim(D)) {
+        *g = kGeom256;
+        return true;
+      }
+      return false;
   }
 }
 
 template <int DT>
 int dispatch(const PrefillParams &p, int D, int max_len, int plan_len, hipStream_t s) {
   if (pipe_dim(D)) return prefill_pipe_dispatch(p, DT, D, max_len, plan_len, s);
+  constexpr int KT = kGeom256.kt, NW = DD_PREFILL_NW;
   switch (D) {
-    case 256: return launch<DT, 256, 1, kGeom256.kt, DD_PREFILL_NW>(p, max_len, plan_len, s);
+    case 144: return launch<DT, 256, 1, KT, NW, 144>(p, max_len, plan_len, s);
+    case 160: return launch<DT, 256, 1, KT, NW, 160>(p, max_len, plan_len, s);
+    case 176: return launch<DT, 256, 1, KT, NW, 176>(p, max_len, plan_len, s);
+    case 192: return launch<DT, 256, 1, KT, NW, 192>(p, max_len, plan_len, s);
+    case 208: return launch<DT, 256, 1, KT, NW, 208>(p, max_len, plan_len, s);
+    case 224: return launch<DT, 256, 1, KT, NW, 224>(p, max_len, plan_len, s);
+    case 240: return launch<DT, 256, 1, KT, NW, 240>(p, max_len, plan_len, s);
+    case 256: return launch<DT, 256, 1, KT, NW>(p, max_len, plan_len, s);
     default: return DD_EUNSUPPORTED;
   }
 }
@@ -582,7 +625,9 @@ static int prefill_entry(int phase, const void *q, const void *k, const void *v,
     const int rc = dd_prefill_f32(args, dtype, s);
     return rc != DD_EUNSUPPORTED ? rc : dd_prefill_generic(args, dtype, s);
   };
-  if (dtype == DD_F32 || !geometry(dim, &geom) || scale == 0.f) return (phase & 1) ? exact(a) : DD_OK;
+  // (and more query heads per KV head than one 16-bit work item has columns)
+  if (dtype == DD_F32 || !geometry(dim, &geom) || geom.cols < heads / kv_heads || scale == 0.f)
+    return (phase & 1) ? exact(a) : DD_OK;
   p.scale_log2 = __builtin_fabsf(scale) * kLog2e;
   p.q_sign = scale < 0.f ? 0x80008000u : 0u;
   p.flags = needs_flags > 0 ? flags : nullptr;
@@ -628,7 +673,7 @@ extern "C" int dd_prefill_flag_count(int n, int max_len, int heads, int kv_heads
   // only bf16 pages at the head sizes of prefill_pipe_kernel convert V to fp16
   if (dtype != DD_BF16 || !pipe_dim(dim)) return 0;
   const int rows = kGeom128.cols / (heads / kv_heads);
-  if (rows < 1) return 0;   // more heads per KV head than one item holds: not supported at all
+  if (rows < 1) return 0;   // more heads per KV head than one item holds: the exact kernel takes the call
   const long count = (long)n * kv_heads * dd_cdiv(max_len, rows);
   return count > 0x7fffffffL ? -DD_EUNSUPPORTED : (int)count;
 }

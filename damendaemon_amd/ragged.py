@@ -36,11 +36,12 @@ def _check(query, cache_k, cache_v, page_table):
     return query
 
 
-def _has_mfma_geometry(dim):
-    """Whether the 16-bit MFMA prefill kernels take this head size (then the
-    call carries a workgroup plan)."""
+def _has_mfma_geometry(dim, group):
+    """Whether the 16-bit MFMA prefill kernels take this head size and number
+    of query heads per KV head (then the call carries a workgroup plan)."""
     cols, keys = ctypes.c_int(0), ctypes.c_int(0)
-    return _native.library().dd_prefill_geometry(int(dim), ctypes.byref(cols), ctypes.byref(keys)) == 0
+    ok = _native.library().dd_prefill_geometry(int(dim), ctypes.byref(cols), ctypes.byref(keys)) == 0
+    return ok and cols.value >= group
 
 
 def prefill_plan(lengths, starts, heads, kv_heads, dim, window=0, slots=None, workgroups=0):
@@ -113,7 +114,7 @@ def prepare_prefill(query, cache_k, cache_v, packed, page_table, window=0, scale
     max_len = max(packed.lengths[a:b])
     max_context = max(s + n for s, n in zip(packed.starts[a:b], packed.lengths[a:b]))
     plan_dev, plan_len = None, 0
-    if q.dtype != torch.float32 and scale != 0.0 and _has_mfma_geometry(D):
+    if q.dtype != torch.float32 and scale != 0.0 and _has_mfma_geometry(D, H // cache_k.shape[1]):
         # the MFMA kernel's XCD-balanced workgroup order (the fp32 / other-D
         # kernel takes none)
         plan = prefill_plan(packed.lengths[a:b], packed.starts[a:b], H, cache_k.shape[1], D, window,

@@ -156,8 +156,9 @@ def test_prefill_fp32_groups_pages(dim, heads, kvh, page, window, scale):
 @pytest.mark.parametrize('dim', [16, 48, 112, 160, 176, 192, 240, 256])
 @pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16, torch.float16])
 def test_prefill_fp32_arithmetic_head_sizes(dim, dtype):
-    """Head sizes in steps of 16 on the fp32-arithmetic matrix-core kernel (fp32 pages at
-    any of them; 16-bit pages where no 16-bit MFMA kernel exists, D 256 aside)."""
+    """Head sizes in steps of 16: fp32 pages on the fp32-arithmetic matrix-core kernel at
+    every one; 16-bit pages on it at D 16, on the 16-bit kernels' 64 / 128 layouts at
+    D 48 / 112 and on the 256 layout above 128."""
     out, exp = run_segments([1, 45, 100], [0, 70, 260], 12, 4, dim, dtype, seed=dim + 3, window=90)
     check(out, exp, atol=2e-5 if dtype == torch.float32 else 2e-3)
 
@@ -168,6 +169,28 @@ def test_prefill_other_head_sizes(dtype, dim):
     """Head sizes the 16-bit MFMA kernel takes inside its 64 / 128 layouts
     (the dims past the real head size are zeros no MFMA reads)."""
     out, exp = run_segments([3, 64, 100], [0, 200, 17], 12, 4, dim, dtype, seed=dim)
+    check(out, exp)
+
+
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize('dim', [144, 160, 176, 192, 208, 224, 240])
+def test_prefill_wide_head_sizes(dtype, dim):
+    """Head sizes between 128 and 256 on the 16-bit kernel's 256 layout (rows
+    of the real length; the dims past it are zeros the MFMAs skip)."""
+    out, exp = run_segments([3, 64, 100], [0, 200, 17], 12, 4, dim, dtype, seed=dim)
+    check(out, exp)
+
+
+@pytest.mark.parametrize('dim', [160, 224])
+@pytest.mark.parametrize('page,window,heads,kvh', [(16, 0, 32, 8), (32, 70, 8, 1), (16, 0, 40, 2),
+                                                   (16, 300, 130, 1)])
+def test_prefill_wide_head_sizes_pages_windows(dim, page, window, heads, kvh):
+    """The 256 layout with larger pages, windows, wide groups, and more query
+    heads per KV head than its 128-column work item (130: the exact kernel)."""
+    lengths = [1, 77, 200] if heads <= 40 else [1, 9, 40]
+    starts = [5, 0, 1500] if heads <= 40 else [0, 17, 100]
+    out, exp = run_segments(lengths, starts, heads, kvh, dim, torch.bfloat16, seed=dim + page + window + heads,
+                            window=window, page=page)
     check(out, exp)
 
 
@@ -268,7 +291,8 @@ def _scaled_v_case(lengths, starts, heads, kvh, dim, seed, magnitude):
     return case, q, slots
 
 
-@pytest.mark.parametrize('dim,heads,kvh', [(128, 16, 4), (64, 8, 2), (128, 130, 1), (96, 16, 4), (256, 16, 2)])
+@pytest.mark.parametrize('dim,heads,kvh', [(128, 16, 4), (64, 8, 2), (128, 130, 1), (96, 16, 4), (256, 16, 2),
+                                            (160, 16, 4)])
 @pytest.mark.parametrize('spread', ['rows', 1e-6, 1e-5, 3e-3, 2e5, 1e6])
 def test_prefill_bf16_value_range(dim, heads, kvh, spread):
     """bf16 V over the whole bf16 range that matters: per-row magnitudes
@@ -317,7 +341,7 @@ def test_prefill_bf16_one_huge_key():
 
 
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize('dim', [64, 128, 256, 96])
+@pytest.mark.parametrize('dim', [64, 128, 256, 96, 160])
 def test_prefill_scale_zero(dtype, dim):
     """scale 0: every allowed key gets the same weight (SDPA's result for a
     zero scale), windowed or not."""

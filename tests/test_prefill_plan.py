@@ -15,7 +15,7 @@ def _geometry(dim):
     return cols.value, kt.value
 
 
-DIMS = (48, 64, 80, 96, 112, 128, 256)               # head sizes with a 16-bit MFMA kernel
+DIMS = (48, 64, 80, 96, 112, 128, 160, 224, 256)    # head sizes with a 16-bit MFMA kernel
 ROWS = {d: _geometry(d)[0] for d in DIMS}   # (query row, head) columns per workgroup
 KT = {d: _geometry(d)[1] for d in DIMS}     # keys per tile
 
@@ -84,10 +84,17 @@ def test_plan_rejects_bad_arguments():
     with pytest.raises(Exception):
         ragged.prefill_plan([4], [0], 6, 4, 128)     # heads not a multiple of kv_heads
     with pytest.raises(Exception):
-        ragged.prefill_plan([4], [0], 8, 2, 160)     # no 16-bit MFMA kernel for head dim 160
+        ragged.prefill_plan([4], [0], 8, 2, 152)     # no 16-bit MFMA kernel for head dim 152
+    with pytest.raises(Exception):
+        ragged.prefill_plan([4], [0], 130, 1, 160)   # more heads per KV head than an item's 128 columns
     assert len(ragged.prefill_plan([], [], 8, 2, 128)) == 0
     cols, kt = ctypes.c_int(), ctypes.c_int()
-    assert _native.library().dd_prefill_geometry(160, ctypes.byref(cols), ctypes.byref(kt)) != 0
+    assert _native.library().dd_prefill_geometry(152, ctypes.byref(cols), ctypes.byref(kt)) != 0
+    assert _native.library().dd_prefill_geometry(16, ctypes.byref(cols), ctypes.byref(kt)) != 0
+    # the 256 layout takes the multiples of 16 above 128
+    for dim in (144, 160, 240, 256):
+        assert _native.library().dd_prefill_geometry(dim, ctypes.byref(cols), ctypes.byref(kt)) == 0
+        assert (cols.value, kt.value) == (128, 32)
 
 
 @pytest.mark.parametrize('seed', range(4))
