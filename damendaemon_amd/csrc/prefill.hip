@@ -10,8 +10,9 @@
 // reference gathers start+len tokens with copy_pages before its SDPA.
 //
 // This file holds the C entry point, the host-side workgroup plan, and the
-// 16x16x32 MFMA kernel used for head size 256 (prefill_pipe.hip takes 64
-// and 128, prefill_generic.hip fp32 pages and other head sizes).
+// 16x16x32 MFMA kernel used for head sizes 144-240 (prefill_pipe.hip takes
+// 48-128 and 256, prefill_f32.hip / prefill_generic.hip fp32 pages and the
+// other head sizes).
 //
 // MI355X design of the 16x16x32 kernel:
 //   * a workgroup owns one KV head and 16*NQ*NW (query row, head) columns of
@@ -507,12 +508,17 @@ struct Geometry {
 };
 constexpr Geometry kGeom64{256, 64};   // prefill_pipe_kernel: 8 waves x 32 columns, 64-key tiles
 constexpr Geometry kGeom128{256, 64};
-constexpr Geometry kGeom256{16 * 1 * DD_PREFILL_NW, 32};
+// 256 layout: prefill_pipe_kernel at D 256 (4 waves x 32 columns, 32-key
+// tiles) and prefill_kernel at D 144-240 (DD_PREFILL_NW waves x 16 columns)
+constexpr Geometry kGeom256{128, 32};
+static_assert(16 * DD_PREFILL_NW == kGeom256.cols, "both 256-layout kernels take 128 columns");
 
 // Head sizes prefill_pipe_kernel takes (48 in its 64 layout, 80-112 in its
-// 128 layout).
-static bool pipe_dim(int D) { return D == 48 || D == 64 || D == 80 || D == 96 || D == 112 || D == 128; }
-// Head sizes prefill_kernel takes in its 256 layout.
+// 128 layout, 256).
+static bool pipe_dim(int D) {
+  return D == 48 || D == 64 || D == 80 || D == 96 || D == 112 || D == 128 || D == 256;
+}
+// Head sizes prefill_kernel takes in its 256 layout (256 itself: the pipe kernel).
 static bool wide_dim(int D) { return D > 128 && D <= 256 && D % 16 == 0; }
 
 static bool geometry(int D, Geometry *g) {
@@ -544,7 +550,6 @@ int dispatch(const PrefillParams &p, int D, int max_len, int plan_len, hipStream
     case 208: return launch<DT, 256, 1, KT, NW, 208>(p, max_len, plan_len, s);
     case 224: return launch<DT, 256, 1, KT, NW, 224>(p, max_len, plan_len, s);
     case 240: return launch<DT, 256, 1, KT, NW, 240>(p, max_len, plan_len, s);
-    case 256: return launch<DT, 256, 1, KT, NW>(p, max_len, plan_len, s);
     default: return DD_EUNSUPPORTED;
   }
 }
@@ -640,7 +645,7 @@ static int prefill_entry(int phase, const void *q, const void *k, const void *v,
   if (rc != DD_OK || !p.flags || !(phase & 2)) return rc;
   // the items the bf16 kernel flagged, again in fp32 arithmetic
   a.flags = flags;
-  a.flag_rows = kGeom128.cols / p.G;
+  a.flag_rows = geom.cols / p.G;
   a.flag_tiles = (int)dd_cdiv(max_len, a.flag_rows);
   return exact(a);
 }
@@ -671,8 +676,9 @@ extern "C" int dd_prefill_attention_phase(const void *q, const void *k, const vo
 extern "C" int dd_prefill_flag_count(int n, int max_len, int heads, int kv_heads, int dim, int dtype) {
   if (n < 0 || max_len < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads) return -DD_EINVAL;
   // only bf16 pages at the head sizes of prefill_pipe_kernel convert V to fp16
-  if (dtype != DD_BF16 || !pipe_dim(dim)) return 0;
-  const int rows = kGeom128.cols / (heads / kv_heads);
+  Geometry g;
+  if (dtype != DD_BF16 || !pipe_dim(dim) || !geometry(dim, &g)) return 0;
+  const int rows = g.cols / (heads / kv_heads);
   if (rows < 1) return 0;   // more heads per KV head than one item holds: the exact kernel takes the call
   const long count = (long)n * kv_heads * dd_cdiv(max_len, rows);
   return count > 0x7fffffffL ? -DD_EUNSUPPORTED : (int)count;

@@ -1,4 +1,4 @@
-// Chunked-prefill attention for head sizes 48, 64, 80, 96, 112 and 128
+// Chunked-prefill attention for head sizes 48, 64, 80, 96, 112, 128 and 256
 // (gfx950), bf16 or fp16 pages (48 in the 64 layout, 80-112 in the 128
 // layout: the missing dims are zeros in LDS that no MFMA reads); semantics as in prefill.hip (damendaemon/paged.py:97-111 with
 // qwen2.py:754-770): query row j of segment i attends keys 0 .. start_i + j
@@ -10,6 +10,9 @@
 // wave; keys stream in 64-key tiles (four 16-token chunks).  Per tile and
 // wave the matrix cores do 16 MFMAs of S^T = K Q^T and 16 of O^T += V^T P^T
 // (v_mfma_f32_32x32x16), 1024 cycles; the softmax is ~100 VALU operations.
+// The 256 layout: four waves (one per SIMD, each with the SIMD's whole
+// register file: its O^T alone is 128 registers) own 128 columns, and keys
+// stream in 32-key tiles, so that the same K and V rings fit the LDS.
 //
 // Step structure.  Step t of a wave issues the MFMAs of S(t+1) = K(t+1) Q^T
 // and O += V(t)^T P(t) back to back, then the vector work of tile t+1:
@@ -143,24 +146,35 @@ DD_DEV u32x4 bf16x8_to_f16x8(u32x4 x) {
   return y;
 }
 
-// D is the LDS layout's head size (64 or 128); DR <= D the real one (a
+// Waves per workgroup and keys per tile of a layout.  The 256 layout has one
+// wave per SIMD (its 32 columns' O^T alone is 128 registers; the wave gets
+// the SIMD's whole register file) and 32-key tiles (so the rings still fit
+// the LDS).
+template <int D>
+constexpr int pipe_waves() { return D == 256 ? 4 : 8; }
+template <int D>
+constexpr int pipe_keys() { return D == 256 ? 32 : 64; }
+
+// D is the LDS layout's head size (64, 128 or 256); DR <= D the real one (a
 // multiple of 16 above D / 2): rows are DR elements long in memory, the
 // layout's dims DR .. D-1 are loaded as zeros and skipped by the MFMAs.
 template <int DT, int D, int DR>
-__global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
-  static_assert(D == 64 || D == 128, "layouts for head sizes 64 and 128");
+__global__ __launch_bounds__(64 * pipe_waves<D>()) __attribute__((amdgpu_waves_per_eu(pipe_waves<D>() / 4)))
+void prefill_pipe_kernel(PrefillParams p) {
+  static_assert(D == 64 || D == 128 || D == 256, "layouts for head sizes 64, 128 and 256");
   static_assert(DR % 16 == 0 && DR <= D && 2 * DR > D, "real head size");
   constexpr int NCCR = DR / 16;         // k-steps of S^T over the real dims
   constexpr int MDR = (DR + 31) / 32;   // 32-dim blocks of O^T holding real dims
-  constexpr int NW = 8;
+  constexpr int NW = pipe_waves<D>();
   constexpr int NT = 64 * NW;
-  constexpr int KT = 64;                // keys per tile
+  constexpr int KT = pipe_keys<D>();    // keys per tile
+  constexpr int NSB = KT / 32;          // 32-key blocks of S^T per tile
   constexpr int MD = D / 32;            // 32-dim blocks of O^T
   constexpr int DQ = D / 32;            // 1 KiB K blocks per 16-key chunk
   constexpr int COLS = 32 * NW;
   constexpr int PLANE = KT * D * 2;     // bytes of one K or V tile
-  constexpr int IPW = DQ / 2;           // K DMA instructions per wave per tile
-  static_assert(IPW == 1 || IPW == 2, "one or two 1 KiB blocks per wave and operand");
+  constexpr int IPW = (KT / 16) * DQ / NW;   // K DMA instructions per wave per tile
+  static_assert(IPW >= 1 && IPW <= 4 && DQ % IPW == 0, "one to four 1 KiB blocks per wave and operand, one chunk");
   constexpr int VJ = PLANE / (16 * NT); // 16-byte pieces per thread of a V tile
   // loads issued after V(kt+2) that may still be in flight when this wave's
   // K(kt+2) and V(kt+2) must have landed (end of step kt): the K/V loads of
@@ -249,12 +263,13 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   const int k_chunk = kb0 / DQ;
   // lanes whose 8 dims lie past the real head size load nothing (an offset
   // past every buffer resource reads as zero)
-  // (IPW <= 2: the per-block offsets are held as two scalars)
+  // (the per-block offsets are held as scalars, not an array a lambda captures)
   auto k_off = [&](int j) {
     const int d0 = 32 * (kb0 % DQ + j) + 8 * (lane >> 4);
     return d0 < DR ? 2u * ((lane & 15) * DR + d0) : 0x80000000u;
   };
-  const unsigned k_dma0 = k_off(0), k_dma1 = DR == D ? 0u : k_off(1);
+  const unsigned k_dma0 = k_off(0), k_dma1 = DR == D || IPW < 2 ? 0u : k_off(1),
+                 k_dma2 = DR == D || IPW < 3 ? 0u : k_off(2), k_dma3 = DR == D || IPW < 4 ? 0u : k_off(3);
   // Page of one 16-key chunk of tile kt (-1: none, or past the last tile).
   // The lookups for a step's loads are read from LDS during the previous
   // step, so that no step starts by waiting for one.
@@ -281,8 +296,9 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
       if constexpr (DR == D)   // block j is 32 dims (64 bytes) further along the row
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(dst + j * 1024), 16, k_dma0, 64 * j, 0, 0);
       else
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(dst + j * 1024), 16, j == 0 ? k_dma0 : k_dma1, 0,
-                                                 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (lds_void *)(dst + j * 1024), 16, j == 0 ? k_dma0 : j == 1 ? k_dma1 : j == 2 ? k_dma2 : k_dma3, 0, 0,
+            0);
   };
   // V: blocks (chunk, md) of 1 KiB, the same chunk as K; DMA lane m of block
   // (c, md) brings the 16 bytes V[16c + 8(m/32) + 4((m%32)/16) + ((m%32)/2)%4]
@@ -296,7 +312,8 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
     const int q8 = 4 * (vb0 % MD + j) + 2 * ((m >> 3) & 1) + (m & 1);
     return 8 * q8 < DR ? (unsigned)(key * DR * 2 + 16 * q8) : 0x80000000u;
   };
-  const unsigned v_dma0 = v_off(0), v_dma1 = DR == D ? 0u : v_off(1);
+  const unsigned v_dma0 = v_off(0), v_dma1 = DR == D || IPW < 2 ? 0u : v_off(1),
+                 v_dma2 = DR == D || IPW < 3 ? 0u : v_off(2), v_dma3 = DR == D || IPW < 4 ? 0u : v_off(3);
   auto issue_v = [&](int kt, int phys) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(p.v, kt, k_chunk, phys);
     char *dst = s_v + ((kt - kt_first) % NVS) * PLANE + vb0 * 1024;
@@ -305,8 +322,9 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
       if constexpr (DR == D)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(dst + j * 1024), 16, v_dma0, 64 * j, 0, 0);
       else
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(dst + j * 1024), 16, j == 0 ? v_dma0 : v_dma1, 0,
-                                                 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (lds_void *)(dst + j * 1024), 16, j == 0 ? v_dma0 : j == 1 ? v_dma1 : j == 2 ? v_dma2 : v_dma3, 0, 0,
+            0);
   };
   const unsigned v_base = lds_addr(s_v);
   // bf16 V tile kt -> fp16 in place (16 contiguous bytes per lane), in two
@@ -335,12 +353,12 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
 
   // ---- S^T of one tile: two 32-key blocks ----
   const unsigned k_rd = lds_addr(s_k) + 1024u * DQ * ((lane >> 4) & 1) + 16u * (lane & 15) + 256u * h2;
-  auto compute_s = [&](int kt, f32x16 (&s)[2]) __attribute__((always_inline)) {
+  auto compute_s = [&](int kt, f32x16 (&s)[NSB]) __attribute__((always_inline)) {
     const unsigned kb_addr = k_rd + (unsigned)(((kt - kt_first) % NKS) * PLANE);
-    // operand i = (cc, b) = (i / 2, i % 2); R reads in flight
-    constexpr int N = 2 * NCCR, R = 4;
+    // operand i = (cc, b) = (i / NSB, i % NSB); R reads in flight
+    constexpr int N = NSB * NCCR, R = 4;
     auto rd = [&](int i) __attribute__((always_inline)) {
-      const int cc = i >> 1, b = i & 1;
+      const int cc = i / NSB, b = i % NSB;
       return lds_read128(kb_addr, (2 * b * DQ + cc / 2) * 1024 + 512 * (cc & 1));
     };
     u32x4 kop[R];
@@ -348,7 +366,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
     for (int i = 0; i < R; ++i) kop[i] = rd(i);
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      const int cc = i >> 1, b = i & 1;
+      const int cc = i / NSB, b = i % NSB;
       lgkm_wait(kop[i % R], min(R - 1, N - 1 - i));
       s[b] = mfma_s<DT>(kop[i % R], qb[cc], cc == 0 ? f32x16{} : s[b]);
       if (i + R < N) kop[i % R] = rd(i + R);
@@ -380,9 +398,9 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
     }
     return mu;
   };
-  // Probabilities 2i, 2i+1 of this lane (i < 16: block i / 8, registers
+  // Probabilities 2i, 2i+1 of this lane (i < 8 NSB: block i / 8, registers
   // 2 (i % 8) ..+2) into the fp16 P^T operands, and into the row sum.
-  auto softmax_pair = [&](f32x16 (&s)[2], int i, float mu, u32x4 (&pp)[2][2], float &lsum)
+  auto softmax_pair = [&](f32x16 (&s)[NSB], int i, float mu, u32x4 (&pp)[NSB][2], float &lsum)
       __attribute__((always_inline)) {
     const int b = i >> 3, r = 2 * (i & 7);
     const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[b][r], sc, -mu));
@@ -392,13 +410,13 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
     lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, h), f16x2{(_Float16)1.f, (_Float16)1.f}, lsum, false);
   };
   // mask of tile kt (keys past a column's diagonal or before its window);
-  // key of register r of block b is kt*64 + 32b + 8(r/4) + 4h2 + r%4
-  auto mask = [&](int kt, f32x16 (&s)[2]) __attribute__((always_inline)) {
+  // key of register r of block b is kt*KT + 32b + 8(r/4) + 4h2 + r%4
+  auto mask = [&](int kt, f32x16 (&s)[NSB]) __attribute__((always_inline)) {
     const int kbase = kt * KT;
     if (!(kbase + KT - 1 <= start + r0 && (p.window == 0 || kbase >= start + r0 + rows_here - p.window))) {
       const int lo = p.window > 0 ? qpos - p.window + 1 : -1;
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
+      for (int b = 0; b < NSB; ++b) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = kbase + 32 * b + 8 * (r >> 2) + 4 * h2 + (r & 3);
@@ -408,11 +426,11 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
     }
   };
   // partial column max over registers 4i .. 4i+3 of both blocks
-  auto max_part = [&](f32x16 (&s)[2], int i, float &mx) __attribute__((always_inline)) {
+  auto max_part = [&](f32x16 (&s)[NSB], int i, float &mx) __attribute__((always_inline)) {
 #pragma unroll
-    for (int b = 0; b < 2; ++b) mx = fmaxf(fmaxf(mx, s[b][4 * i]), s[b][4 * i + 1]);
+    for (int b = 0; b < NSB; ++b) mx = fmaxf(fmaxf(mx, s[b][4 * i]), s[b][4 * i + 1]);
 #pragma unroll
-    for (int b = 0; b < 2; ++b) mx = fmaxf(fmaxf(mx, s[b][4 * i + 2]), s[b][4 * i + 3]);
+    for (int b = 0; b < NSB; ++b) mx = fmaxf(fmaxf(mx, s[b][4 * i + 2]), s[b][4 * i + 3]);
   };
 
   // ---- matrix-core phase of step kt: S(kt+1) = K(kt+1) Q^T (when there is
@@ -420,10 +438,10 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   // operands (one ds_read_b128 each), then V^T operands (two transposing
   // reads each), R operands in flight.  The step's loads are issued after
   // the first MFMAs, so that any wait for the memory pipeline overlaps them.
-  auto mfma_phase = [&](auto has_next_c, int kt, f32x16 (&s)[2], const u32x4 (&pp)[2][2], auto &&loads)
+  auto mfma_phase = [&](auto has_next_c, int kt, f32x16 (&s)[NSB], const u32x4 (&pp)[NSB][2], auto &&loads)
       __attribute__((always_inline)) {
     constexpr bool HN = decltype(has_next_c)::value;
-    constexpr int NS = HN ? 2 * NCCR : 0, NV = 4 * MDR, N = NS + NV, R = DD_PF_RING;
+    constexpr int NS = HN ? NSB * NCCR : 0, NV = 2 * NSB * MDR, N = NS + NV, R = DD_PF_RING;
     const unsigned kb_addr = k_rd + (unsigned)(((kt + 1 - kt_first) % NKS) * PLANE);
     const unsigned vb = v_rd + (unsigned)(((kt - kt_first) % NVS) * PLANE);
     // operand i < NS: one K read; else two transposing reads
@@ -431,7 +449,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
     u32x2 lo[R], hi[R];
     auto rd = [&](int i) __attribute__((always_inline)) {
       if (i < NS) {
-        const int cc = i >> 1, b = i & 1;
+        const int cc = i / NSB, b = i % NSB;
         kop[i % R] = lds_read128(kb_addr, (2 * b * DQ + cc / 2) * 1024 + 512 * (cc & 1));
       } else {
         const int j = i - NS, blk = (j / MDR) * MD + j % MDR;   // (key block, dim block)
@@ -451,7 +469,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       if (i < NS) {
-        const int cc = i >> 1, b = i & 1;
+        const int cc = i / NSB, b = i % NSB;
         lgkm_wait(kop[i % R], after(i));
         s[b] = mfma_s<DT>(kop[i % R], qb[cc], cc == 0 ? f32x16{} : s[b]);
       } else {
@@ -476,7 +494,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   // probability past fp16's range shows up as a non-finite row sum; then
   // the wave redoes the tile with the tile's max (moving the offset and
   // rescaling O and l as usual) ----
-  auto valu_phase = [&](int kt, f32x16 (&s)[2], u32x4 (&pp)[2][2], int &pk)
+  auto valu_phase = [&](int kt, f32x16 (&s)[NSB], u32x4 (&pp)[NSB][2], int &pk)
       __attribute__((always_inline)) {
     u32x4 x[VJ];
     convert_v_read(kt + 1, x);
@@ -485,11 +503,11 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
     const float mu0 = m_run * sc;
     float lsum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) softmax_pair(s, i, mu0, pp, lsum);
+    for (int i = 0; i < 4 * NSB; ++i) softmax_pair(s, i, mu0, pp, lsum);
     // V(kt+1) of every wave landed before the previous barrier
     convert_v_write(kt + 1, x);
 #pragma unroll
-    for (int i = 8; i < 16; ++i) softmax_pair(s, i, mu0, pp, lsum);
+    for (int i = 4 * NSB; i < 8 * NSB; ++i) softmax_pair(s, i, mu0, pp, lsum);
     if (__builtin_amdgcn_ballot_w64(!(lsum <= 3.0e38f))) {
       float m = kNegInf;
 #pragma unroll
@@ -497,7 +515,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
       const float mu = softmax_begin(xor32_max(m));
       lsum = 0.f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) softmax_pair(s, i, mu, pp, lsum);
+      for (int i = 0; i < 8 * NSB; ++i) softmax_pair(s, i, mu, pp, lsum);
     }
     l_part += lsum;
     // this wave's K(kt+2) and V(kt+2) land before the next barrier
@@ -505,8 +523,8 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   };
 
   // ---- prologue: K and V of tiles f .. f+NKS-1 in flight, V(f) in fp16, P(f) ----
-  f32x16 s[2];
-  u32x4 pp[2][2];   // P(kt) as fp16 P^T operands
+  f32x16 s[NSB];
+  u32x4 pp[NSB][2];   // P(kt) as fp16 P^T operands
   // All the prologue's loads go out together, each without a branch (see
   // table_entry_nb): the first tiles' page numbers, then the item's
   // page-table entries for the LDS copy and Q; then, once the page numbers
@@ -566,7 +584,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
     const float mu = softmax_begin(xor32_max(m));
     float lsum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) softmax_pair(s, i, mu, pp, lsum);
+    for (int i = 0; i < 8 * NSB; ++i) softmax_pair(s, i, mu, pp, lsum);
     l_part += lsum;
   }
   barrier();   // every wave has read K(kt_first) before step kt_first reloads its slot
@@ -627,7 +645,7 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
   lgkm_drain();
   barrier();
   constexpr int ORS = 2 * DR + 16;      // LDS row stride of the output tile
-  static_assert(8 * 32 * ORS <= NVS * PLANE, "output tile fits the V ring");
+  static_assert(NW * 32 * ORS <= NVS * PLANE, "output tile fits the V ring");
   char *otile = s_v + w * 32 * ORS;
   if (colok) {
     const float inv = 1.f / l;
@@ -663,13 +681,13 @@ __global__ __launch_bounds__(512) void prefill_pipe_kernel(PrefillParams p) {
 
 template <int DT, int D, int DR = D>
 int launch_pipe(PrefillParams p, int max_len, int plan_len, hipStream_t s) {
-  constexpr int COLS = 256;
+  constexpr int COLS = 32 * pipe_waves<D>();
   if (COLS / p.G < 1) return DD_EUNSUPPORTED;
   p.max_tiles = (int)dd_cdiv(max_len, COLS / p.G);
   const long grid = p.plan ? (long)plan_len : 8L * dd_cdiv((long)p.n * p.KH, 8) * p.max_tiles;
   if (grid == 0) return DD_OK;
   if (grid > 0x7fffffffL) return DD_EUNSUPPORTED;
-  hipLaunchKernelGGL((prefill_pipe_kernel<DT, D, DR>), dim3((unsigned)grid), dim3(512), 0, s, p);
+  hipLaunchKernelGGL((prefill_pipe_kernel<DT, D, DR>), dim3((unsigned)grid), dim3(64 * pipe_waves<D>()), 0, s, p);
   DD_LAUNCH_CHECK();
   return DD_OK;
 }
@@ -683,6 +701,7 @@ int pipe_dims(const PrefillParams &p, int dim, int max_len, int plan_len, hipStr
     case 96: return launch_pipe<DT, 128, 96>(p, max_len, plan_len, s);
     case 112: return launch_pipe<DT, 128, 112>(p, max_len, plan_len, s);
     case 128: return launch_pipe<DT, 128>(p, max_len, plan_len, s);
+    case 256: return launch_pipe<DT, 256>(p, max_len, plan_len, s);
     default: return DD_EUNSUPPORTED;
   }
 }
