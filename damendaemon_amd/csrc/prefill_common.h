@@ -1,6 +1,6 @@
-// Shared pieces of the chunked-prefill MFMA kernels (prefill.hip,
-// prefill_pipe.hip): the launch parameters, MFMA wrappers, 16-bit operand
-// packing of the probabilities and the transposing LDS read.
+// Shared pieces of the chunked-prefill kernels (prefill.hip,
+// prefill_pipe.hip): the launch parameters, the plan entry of a work item,
+// 16-bit output packing and buffer-resource constants.
 #pragma once
 
 #include "common.h"
@@ -15,10 +15,6 @@ namespace dd_prefill {
 
 
 constexpr float kNegInf = -__builtin_inff();
-#ifndef DD_PREFILL_TAB
-#define DD_PREFILL_TAB 8192
-#endif
-constexpr int kTabCache = DD_PREFILL_TAB;  // page-table entries staged in LDS (128K keys at page 16)
 
 struct PrefillParams {
   const void *q;       // (T, H, D)
@@ -87,83 +83,10 @@ DD_DEV bool prefill_item(const PrefillParams &p, PrefillItem &it, int round = 0)
   return true;
 }
 
-template <int DT>
-DD_DEV f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
-  if constexpr (DT == DD_BF16) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                   0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
-                                                  0, 0);
-  }
-}
-
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-template <int DT>
-DD_DEV f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
-  if constexpr (DT == DD_BF16) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                   0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
-                                                  0, 0);
-  }
-}
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-
-// Transposing LDS read (ds_read_b64_tr_b16): within each 16-lane group,
-// lane i receives element i%4 of the 8-byte chunks addressed by lanes
-// i/4, 4 + i/4, 8 + i/4 and 12 + i/4.
-DD_DEV u32x2 read_tr16(const unsigned short *p) {
-  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_s16x4 *)(__attribute__((address_space(3))) char *)(p));
-  return __builtin_bit_cast(u32x2, v);
-}
-
-// Eight fp32 probabilities -> one 8 x 16-bit MFMA operand (RNE).
-template <int DT>
-DD_DEV u32x4 pack8(f32x4 x0, f32x4 x1) {
-  u32x4 r;
-  if constexpr (DT == DD_BF16) {
-    r[0] = __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{x0[0], x0[1]}, bf16x2));
-    r[1] = __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{x0[2], x0[3]}, bf16x2));
-    r[2] = __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{x1[0], x1[1]}, bf16x2));
-    r[3] = __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{x1[2], x1[3]}, bf16x2));
-  } else {
-    r[0] = __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{x0[0], x0[1]}, f16x2));
-    r[1] = __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{x0[2], x0[3]}, f16x2));
-    r[2] = __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{x1[0], x1[1]}, f16x2));
-    r[3] = __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{x1[2], x1[3]}, f16x2));
-  }
-  return r;
-}
-
-// The residuals x - hi(x) of eight probabilities whose 16-bit high parts
-// are `hi` (pack8 of the same x0, x1), as one more 8 x 16-bit operand: the
-// P.V product with hi and with this residual carries P to ~2^-17 relative,
-// where one 16-bit rounding would leave 2^-9 (bf16) or 2^-12 (fp16).
-template <int DT>
-DD_DEV float hi_part(unsigned w, int half) {
-  if constexpr (DT == DD_BF16) {
-    return half ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
-  } else {
-    return half ? f16_hi(w) : f16_lo(w);
-  }
-}
-template <int DT>
-DD_DEV u32x4 residual8(f32x4 x0, f32x4 x1, u32x4 hi) {
-  const f32x4 r0 = {x0[0] - hi_part<DT>(hi[0], 0), x0[1] - hi_part<DT>(hi[0], 1), x0[2] - hi_part<DT>(hi[1], 0),
-                    x0[3] - hi_part<DT>(hi[1], 1)};
-  const f32x4 r1 = {x1[0] - hi_part<DT>(hi[2], 0), x1[1] - hi_part<DT>(hi[2], 1), x1[2] - hi_part<DT>(hi[3], 0),
-                    x1[3] - hi_part<DT>(hi[3], 1)};
-  return pack8<DT>(r0, r1);
-}
 
 template <int DT>
 DD_DEV unsigned pack2(float a, float b) {

@@ -701,6 +701,13 @@ int pipe_dims(const PrefillParams &p, int dim, int max_len, int plan_len, hipStr
     case 96: return launch_pipe<DT, 128, 96>(p, max_len, plan_len, s);
     case 112: return launch_pipe<DT, 128, 112>(p, max_len, plan_len, s);
     case 128: return launch_pipe<DT, 128>(p, max_len, plan_len, s);
+    case 144: return launch_pipe<DT, 256, 144>(p, max_len, plan_len, s);
+    case 160: return launch_pipe<DT, 256, 160>(p, max_len, plan_len, s);
+    case 176: return launch_pipe<DT, 256, 176>(p, max_len, plan_len, s);
+    case 192: return launch_pipe<DT, 256, 192>(p, max_len, plan_len, s);
+    case 208: return launch_pipe<DT, 256, 208>(p, max_len, plan_len, s);
+    case 224: return launch_pipe<DT, 256, 224>(p, max_len, plan_len, s);
+    case 240: return launch_pipe<DT, 256, 240>(p, max_len, plan_len, s);
     case 256: return launch_pipe<DT, 256>(p, max_len, plan_len, s);
     default: return DD_EUNSUPPORTED;
   }

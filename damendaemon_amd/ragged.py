@@ -167,7 +167,7 @@ _CU_COUNT = {}
 def _persistent_workgroups(device, dim):
     """Workgroup count for a persistent prefill schedule: one per CU for the
     kernel that runs its items in turn (head sizes up to 128, and 256), else 0."""
-    if dim > 128 and dim != 256:
+    if dim > 256:
         return 0
     forced = os.environ.get('DAMENDAEMON_AMD_PREFILL_WORKGROUPS')   # tuning: 0 = one item per workgroup
     if forced is not None:
