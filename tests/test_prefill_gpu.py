@@ -181,7 +181,7 @@ def test_prefill_wide_head_sizes(dtype, dim):
     check(out, exp)
 
 
-@pytest.mark.parametrize('dim', [160, 224])
+@pytest.mark.parametrize('dim', [160, 224, 256])
 @pytest.mark.parametrize('page,window,heads,kvh', [(16, 0, 32, 8), (32, 70, 8, 1), (16, 0, 40, 2),
                                                    (16, 300, 130, 1)])
 def test_prefill_wide_head_sizes_pages_windows(dim, page, window, heads, kvh):
