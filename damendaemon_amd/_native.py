@@ -119,7 +119,12 @@ class _Staging:
 
     def upload(self, host, device):
         """Asynchronous copy of the contiguous CPU tensor ``host`` to ``device``
-        on the current stream; returns the device tensor."""
+        on the current stream; returns the device tensor.  Not under graph
+        capture: a replay would copy whatever the reused pinned slot holds by
+        then (prepare the call outside the capture and capture its run())."""
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError('host upload during HIP graph capture: prepare the call (prepare_prefill, '
+                               'pack_batch) before capturing and capture only the launch')
         host = host.contiguous()
         with self._lock:
             return self._upload(host, torch.device(device))

@@ -36,3 +36,34 @@ def test_decode_graph_replays_match_eager(kind):
         torch.cuda.synchronize()
         assert torch.equal(launch.out, eager), f'replay {i} differs from the eager launch'
         torch.randn(1024, device=DEV).sum().item()  # unrelated eager work between replays
+
+
+@pytest.mark.parametrize('dim', [128, 256])
+def test_prefill_graph_replays_match_eager(dim):
+    """A prepared prefill launch (plan uploaded, flags allocated) captured in a
+    HIP graph: its persistent schedule and re-run flags replay exactly.  The
+    host-side preparation itself cannot be captured (it uploads through reused
+    pinned buffers) and says so."""
+    from damendaemon_amd import packing, ragged
+    lengths, starts = [1, 70, 300, 129], [0, 40, 900, 2000]
+    contexts = [s + n for s, n in zip(starts, lengths)]
+    case = paged_decode_case(contexts, 16, 4, dim, torch.bfloat16, seed=dim)
+    d = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    q = torch.randn(sum(lengths), 16, dim, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(DEV)
+    packed = packing.pack_batch(lengths, starts, list(range(len(lengths))), d['page_table'])
+    launch = ragged.prepare_prefill(q, d['cache_k'], d['cache_v'], packed, d['page_table'])
+    eager = launch.run().clone()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch.run()
+    for i in range(3):
+        launch.out.fill_(float('nan'))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(launch.out, eager), f'replay {i} differs from the eager launch'
+        torch.randn(1024, device=DEV).sum().item()
+    with pytest.raises(RuntimeError, match='graph capture'):
+        with torch.cuda.graph(torch.cuda.CUDAGraph()):
+            ragged.prepare_prefill(q, d['cache_k'], d['cache_v'], packed, d['page_table'])
