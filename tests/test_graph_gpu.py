@@ -38,6 +38,7 @@ def test_decode_graph_replays_match_eager(kind):
         torch.randn(1024, device=DEV).sum().item()  # unrelated eager work between replays
 
 
+@pytest.mark.filterwarnings('ignore:The CUDA Graph is empty')
 @pytest.mark.parametrize('dim', [128, 256])
 def test_prefill_graph_replays_match_eager(dim):
     """A prepared prefill launch (plan uploaded, flags allocated) captured in a
