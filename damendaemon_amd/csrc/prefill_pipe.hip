@@ -39,11 +39,11 @@
 // (v_dot2_f32_f16, fp32 accumulate) from exactly the fp16 P that the P.V
 // product uses.
 //
-// Memory path (per tile, 4 chunks of 16 tokens; larger pages are read 16
-// rows at a time).  K and V both arrive by direct-to-LDS buffer loads, two
-// (D = 128) or one (D = 64) per wave and operand, issued NKS steps ahead
-// into rings of NKS (K) and NKS + 1 (V) tile slots: the kernel is bound by
-// the bytes each CU keeps in flight against the HBM latency under load.
+// Memory path (per tile, 4 chunks of 16 tokens, 2 in the 256 layout;
+// larger pages are read 16 rows at a time).  K and V both arrive by
+// direct-to-LDS buffer loads of 1 KiB per wave instruction, two (D = 128),
+// one (D = 64) or four (the 256 layout) per wave and operand, issued NKS
+// steps ahead into rings of NKS (K) and NKS + 1 (V) tile slots.
 // Every load goes through a buffer resource that covers only the chunk's
 // live rows: rows past the context and chunks without an allocated page
 // read as zeros.
