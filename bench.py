@@ -91,6 +91,39 @@ def measured_traffic(summary, family='decode'):
     return int(fields['traffic_bytes_per_launch'])
 
 
+def cpu_baseline_mixed(case, n_chunks, budget_s=20.0):
+    """The mixed batch's attention on the host cores the way the reference's
+    executor runs it there: per prefill chunk a page gather and a lower-right
+    causal SDPA (oracle.prefill_attention_sdpa), and the decode rows through
+    oracle.decode_attention_sdpa, fp32, every core of this process."""
+    from oracle import paged_oracle
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    lengths, starts, slots = case['lengths'], case['starts'], case['seg_slots']
+    table, ck, cv, q = (case[k].cpu() for k in ('page_table', 'cache_k', 'cache_v', 'q'))
+    t_pre = sum(lengths[:n_chunks])
+    dec_pos = torch.tensor(starts[n_chunks:], dtype=torch.int64)
+    dec_slots = torch.tensor(slots[n_chunks:], dtype=torch.int64)
+
+    def step():
+        paged_oracle.prefill_attention_sdpa(q[:t_pre], ck, cv, lengths[:n_chunks], starts[:n_chunks],
+                                            slots[:n_chunks], table)
+        paged_oracle.decode_attention_sdpa(q[t_pre:].unsqueeze(2), ck, cv, dec_pos, dec_slots, table)
+
+    step()   # warm-up
+    times = []
+    start = time.perf_counter()
+    while len(times) < 2 or (time.perf_counter() - start < budget_s and len(times) < 5):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {'value': sum(lengths) / med, 'unit': 'tokens/s', 'cores': threads, 'kind': 'port',
+            'sample': f'the whole batch ({n_chunks} chunks of {lengths[0]} tokens + {len(lengths) - n_chunks} '
+                      f'decode rows): fp32 page gather + SDPA per chunk and for the decode rows on {threads} '
+                      f'threads, median of {len(times)} steps'}
+
+
 def build_case(name, device):
     from damendaemon_amd import workloads, kv_quant
     if name == 'c2':
@@ -343,8 +376,10 @@ def bench_mixed(args, dev, dtype=torch.bfloat16):
                    'ragged_attention_ms': ragged_ms,
                    'decode_hbm_gbps': decode_bytes / (decode_ms * 1e-3) / 1e9 if decode_rows else None},
         'roofline': {'bound': 'mfma', 'achieved': tflops, 'peak': peak, 'unit': 'TFLOP/s',
-                     'frac': tflops / peak, 'traffic': None},
-        'cpu_baseline': None}), flush=True)
+                     'frac': tflops / peak,
+                     'traffic': measured_traffic('prefill_c4_pmc', 'prefill') if not f32 and D == 128 else None},
+        'cpu_baseline': None if args.no_cpu_baseline or not decode_rows else cpu_baseline_mixed(case, n_chunks)}),
+        flush=True)
 
 
 def _event_mean_ms(fn, steps, warmup):

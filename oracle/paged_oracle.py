@@ -174,6 +174,30 @@ def decode_attention_sdpa(query, cache_k, cache_v, positions, slots, page_table)
                                           enable_gqa=True)
 
 
+def prefill_attention_sdpa(query, cache_k, cache_v, lengths, starts, slots, page_table):
+    """fp32 chunked prefill the way the reference's executor runs it on the
+    CPU: per segment, gather the slot's start+len tokens from the pages
+    (damendaemon/paged.py:101-104, copy_pages) and call SDPA with the
+    lower-right causal mask (qwen2.py:754-770, GQA by repeating the KV
+    heads).  Used as the CPU baseline of bench.py's mixed-batch line and
+    cross-checked against ``prefill_attention`` in tests/test_oracle.py.
+    """
+    T, H, D = query.shape
+    KH, page = cache_k.shape[1], cache_k.shape[2]
+    out = torch.empty((T, H, D), dtype=torch.float32)
+    t0 = 0
+    for n, s, slot in zip(lengths, starts, slots):
+        npages = -(-(s + n) // page)
+        rows = page_table[slot, :npages].long()     # the slot's pages, gathered at once
+        k = cache_k[rows].transpose(0, 1).reshape(KH, npages * page, D)[:, :s + n].float()   # (KH, s+n, D)
+        v = cache_v[rows].transpose(0, 1).reshape(KH, npages * page, D)[:, :s + n].float()
+        q = query[t0:t0 + n].float().transpose(0, 1)                     # (H, n, D)
+        mask = torch.arange(s + n)[None, :] <= (s + torch.arange(n))[:, None]   # row j sees keys <= s + j
+        out[t0:t0 + n] = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, enable_gqa=KH != H).transpose(0, 1)
+        t0 += n
+    return out
+
+
 # ---------------------------------------------------------------------------
 # a4: host packer (damendaemon/paged.py:149-159, 118-120; batch.py:133-140)
 
@@ -312,6 +336,8 @@ def prefill_attention(query, cache_k, cache_v, lengths, starts, slots, page_tabl
 # ---------------------------------------------------------------------------
 # How each function is pinned (exercised in tests/test_oracle.py).
 PINNING = {
+    'prefill_attention_sdpa': 'prefill_attention (float64 loop) on seeded ragged segments with GQA and '
+                              'histories of several pages (tests/test_oracle.py)',
     'gather_pages': 'brute-force page walk vs torch.cat of pages '
                     '(scripts/verify_paged_copies.py:15-24 construction); permutation invariance',
     'copy_pages': 'gather/restore round trip; untouched tails stay bit-identical',

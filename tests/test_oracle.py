@@ -204,6 +204,19 @@ def test_prefill_oracle_matches_sdpa_lower_right():
         t0 += n
 
 
+def test_prefill_sdpa_baseline_matches_oracle():
+    """The vectorised fp32 gather + SDPA prefill (bench.py's CPU baseline of
+    the mixed batch) against the float64 loop, GQA 4:1, histories spanning
+    several pages, a single-row segment and a segment without history."""
+    case = paged_decode_case([1, 47, 300, 33], 8, 2, 64, torch.float32, seed=13)
+    lengths, starts, slots = [1, 40, 129, 33], [0, 7, 171, 0], [0, 1, 2, 3]
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(sum(lengths), 8, 64, generator=g)
+    want = O.prefill_attention(q, case['cache_k'], case['cache_v'], lengths, starts, slots, case['page_table'])
+    got = O.prefill_attention_sdpa(q, case['cache_k'], case['cache_v'], lengths, starts, slots, case['page_table'])
+    assert got.dtype == torch.float32 and torch.allclose(got.double(), want, atol=2e-6)
+
+
 @pytest.mark.parametrize('window', [1, 5, 33, 200])
 def test_prefill_oracle_window_matches_sdpa_explicit_mask(window):
     """The windowed prefill of qwen2.py:765-770: keys with kpos <= qpos and
