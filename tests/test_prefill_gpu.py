@@ -88,19 +88,23 @@ def test_prefill_running_max_moves(dtype, slope):
     check(out, exp)
 
 
-def test_mixed_batch_end_to_end():
-    """Config C4 at reduced size: pack on the GPU, write the new K/V into the pages, attend."""
-    rng = random.Random(4)
-    heads, kvh, dim = 32, 8, 128
+@pytest.mark.parametrize('dim,dtype', [(128, torch.bfloat16), (256, torch.bfloat16), (96, torch.float16),
+                                       (64, torch.float16)])
+def test_mixed_batch_end_to_end(dim, dtype):
+    """Config C4 at reduced size: pack on the GPU, write the new K/V into the pages, attend
+    (prefill chunks and decode rows on their two streams), at the head sizes both the decode
+    and the 16-bit prefill kernels take."""
+    rng = random.Random(4 + dim)
+    heads, kvh = 32, 8
     starts = [rng.randint(0, 1024) for _ in range(3)] + [rng.randint(256, 2048) - 1 for _ in range(20)]
     lengths = [128] * 3 + [1] * 20
     contexts = [s + n for s, n in zip(starts, lengths)]
-    case = paged_decode_case(contexts, heads, kvh, dim, torch.bfloat16, seed=44, nan_fill=True)
+    case = paged_decode_case(contexts, heads, kvh, dim, dtype, seed=44, nan_fill=True)
     g = torch.Generator().manual_seed(45)
     T = sum(lengths)
-    q = torch.randn(T, heads, dim, generator=g).to(torch.bfloat16)
-    k_new = torch.randn(T, kvh, dim, generator=g).to(torch.bfloat16)
-    v_new = torch.randn(T, kvh, dim, generator=g).to(torch.bfloat16)
+    q = torch.randn(T, heads, dim, generator=g).to(dtype)
+    k_new = torch.randn(T, kvh, dim, generator=g).to(dtype)
+    v_new = torch.randn(T, kvh, dim, generator=g).to(dtype)
     slots = list(range(len(lengths)))
     table = case['page_table'].to(DEV)
     ck, cv = case['cache_k'].to(DEV), case['cache_v'].to(DEV)
