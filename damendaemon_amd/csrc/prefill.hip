@@ -32,21 +32,22 @@ struct Geometry {
   int cols, kt;
 };
 // prefill_pipe_kernel's layouts: 8 waves x 32 columns and 64-key tiles for
-// the 64 and 128 layouts, 4 waves x 32 columns and 32-key tiles for the 256
-// layout (prefill_pipe.hip: pipe_waves, pipe_keys).
+// the 64, 128 and 160 layouts, 4 waves x 32 columns and 32-key tiles for the
+// 256 layout (prefill_pipe.hip: pipe_waves, pipe_keys).
 constexpr Geometry kGeom64{256, 64};
 constexpr Geometry kGeom128{256, 64};
+constexpr Geometry kGeom160{256, 64};
 constexpr Geometry kGeom256{128, 32};
 
 // Head sizes prefill_pipe_kernel takes: 48 in its 64 layout, 80-112 in its
-// 128 layout, the multiples of 16 above 128 in its 256 layout.
+// 128 layout, 144 in its 160 layout, 176-240 in its 256 layout.
 static bool pipe_dim(int D) {
   return D == 48 || D == 64 || D == 80 || D == 96 || D == 112 || D == 128 || (D > 128 && D <= 256 && D % 16 == 0);
 }
 
 static bool geometry(int D, Geometry *g) {
   if (!pipe_dim(D)) return false;
-  *g = D <= 64 ? kGeom64 : D <= 128 ? kGeom128 : kGeom256;
+  *g = D <= 64 ? kGeom64 : D <= 128 ? kGeom128 : D <= 160 ? kGeom160 : kGeom256;
   return true;
 }
 

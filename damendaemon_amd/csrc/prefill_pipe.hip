@@ -1,6 +1,7 @@
-// Chunked-prefill attention for head sizes 48, 64, 80, 96, 112, 128 and 256
-// (gfx950), bf16 or fp16 pages (48 in the 64 layout, 80-112 in the 128
-// layout: the missing dims are zeros in LDS that no MFMA reads); semantics as in prefill.hip (damendaemon/paged.py:97-111 with
+// Chunked-prefill attention for head sizes 48 to 256 in steps of 16 (gfx950;
+// 16 and 32 excepted), bf16 or fp16 pages, in four LDS layouts: 64 (48, 64),
+// 128 (80-128), 160 (144, 160) and 256 (176-256); below a layout's size the
+// missing dims are zeros in LDS that no MFMA reads.  Semantics as in prefill.hip (damendaemon/paged.py:97-111 with
 // qwen2.py:754-770): query row j of segment i attends keys 0 .. start_i + j
 // of its slot (and > position - window), GQA head h reads KV head h / G,
 // softmax(q.k * scale) . v accumulated in fp32.
@@ -10,9 +11,11 @@
 // wave; keys stream in 64-key tiles (four 16-token chunks).  Per tile and
 // wave the matrix cores do 16 MFMAs of S^T = K Q^T and 16 of O^T += V^T P^T
 // (v_mfma_f32_32x32x16), 1024 cycles; the softmax is ~100 VALU operations.
-// The 256 layout: four waves (one per SIMD, each with the SIMD's whole
-// register file: its O^T alone is 128 registers) own 128 columns, and keys
-// stream in 32-key tiles, so that the same K and V rings fit the LDS.
+// The 160 layout has the same split with three K slots instead of four
+// (its 20 KiB tiles).  The 256 layout: four waves (one per SIMD, each with
+// the SIMD's whole register file: its O^T alone is 128 registers) own 128
+// columns, and keys stream in 32-key tiles, so that the same K and V rings
+// fit the LDS.
 //
 // Step structure.  Step t of a wave issues the MFMAs of S(t+1) = K(t+1) Q^T
 // and O += V(t)^T P(t) back to back, then the vector work of tile t+1:
@@ -42,7 +45,8 @@
 // Memory path (per tile, 4 chunks of 16 tokens, 2 in the 256 layout;
 // larger pages are read 16 rows at a time).  K and V both arrive by
 // direct-to-LDS buffer loads of 1 KiB per wave instruction, two (D = 128),
-// one (D = 64) or four (the 256 layout) per wave and operand, issued NKS
+// one (D = 64), three (the 160 layout, one of them empty for half of the
+// waves) or four (the 256 layout) per wave and operand, issued NKS
 // steps ahead into rings of NKS (K) and NKS + 1 (V) tile slots.
 // Every load goes through a buffer resource that covers only the chunk's
 // live rows: rows past the context and chunks without an allocated page
@@ -77,8 +81,7 @@ namespace {
 #ifndef DD_PF_TAB
 #define DD_PF_TAB 3584
 #endif
-constexpr int NKS = DD_PF_NKS;     // K tile slots: K(kt+NKS) and V(kt+NKS) are issued at step kt
-constexpr int NVS = NKS + 1;       // V tile slots: V(kt) is read while V(kt+1) is converted
+constexpr int kNKS = DD_PF_NKS;    // K tile slots: K(kt+NKS) and V(kt+NKS) are issued at step kt
 constexpr int kTabP = DD_PF_TAB;   // page-table entries staged in LDS per work item
    // page-table entries staged in LDS per work item
 
@@ -154,14 +157,25 @@ template <int D>
 constexpr int pipe_waves() { return D == 256 ? 4 : 8; }
 template <int D>
 constexpr int pipe_keys() { return D == 256 ? 32 : 64; }
+// K tile slots of a layout: three in the 160 layout, whose 20 KiB tiles
+// leave room for no more (3 K + 4 V slots + the staged table: 155 KiB).
+template <int D>
+constexpr int pipe_nks() { return D == 160 ? 3 : kNKS; }
+// LDS operands in flight in the matrix-core phase (fewer in the 160 layout,
+// whose Q and O^T registers leave less room)
+#ifndef DD_PF_RING160
+#define DD_PF_RING160 4
+#endif
+template <int D>
+constexpr int pipe_ring() { return D == 160 ? DD_PF_RING160 : DD_PF_RING; }
 
-// D is the LDS layout's head size (64, 128 or 256); DR <= D the real one (a
+// D is the LDS layout's head size (64, 128, 160 or 256); DR <= D the real one (a
 // multiple of 16 above D / 2): rows are DR elements long in memory, the
 // layout's dims DR .. D-1 are loaded as zeros and skipped by the MFMAs.
 template <int DT, int D, int DR>
 __global__ __launch_bounds__(64 * pipe_waves<D>()) __attribute__((amdgpu_waves_per_eu(pipe_waves<D>() / 4)))
 void prefill_pipe_kernel(PrefillParams p) {
-  static_assert(D == 64 || D == 128 || D == 256, "layouts for head sizes 64, 128 and 256");
+  static_assert(D == 64 || D == 128 || D == 160 || D == 256, "layouts for head sizes 64, 128, 160 and 256");
   static_assert(DR % 16 == 0 && DR <= D && 2 * DR > D, "real head size");
   constexpr int NCCR = DR / 16;         // k-steps of S^T over the real dims
   constexpr int MDR = (DR + 31) / 32;   // 32-dim blocks of O^T holding real dims
@@ -173,17 +187,31 @@ void prefill_pipe_kernel(PrefillParams p) {
   constexpr int DQ = D / 32;            // 1 KiB K blocks per 16-key chunk
   constexpr int COLS = 32 * NW;
   constexpr int PLANE = KT * D * 2;     // bytes of one K or V tile
-  constexpr int IPW = (KT / 16) * DQ / NW;   // K DMA instructions per wave per tile
-  static_assert(IPW >= 1 && IPW <= 4 && DQ % IPW == 0, "one to four 1 KiB blocks per wave and operand, one chunk");
-  constexpr int VJ = PLANE / (16 * NT); // 16-byte pieces per thread of a V tile
+  constexpr int NKS = pipe_nks<D>();    // K tile slots
+  constexpr int NVS = NKS + 1;          // V tile slots: V(kt) is read while V(kt+1) is converted
+  constexpr int NBLK = (KT / 16) * DQ;  // 1 KiB blocks of a K (or V) tile
+  // The 160 layout's 20 blocks (5 per chunk) go to the 8 waves as 3 + 2 per
+  // chunk: a wave with two issues a third load that reads nothing (offset
+  // past its resource) into a scratch block, so that every wave issues the
+  // same number of loads and every wait count stays static.
+  constexpr bool SPLIT = NBLK % NW != 0;
+  constexpr int IPW = (NBLK + NW - 1) / NW;  // K DMA instructions per wave per tile
+  static_assert(IPW >= 1 && IPW <= 4, "one to four 1 KiB blocks per wave and operand");
+  static_assert(SPLIT ? (DQ == 5 && NW == 2 * (KT / 16) && IPW == 3) : DQ % IPW == 0,
+                "a wave's blocks lie in one chunk");
+  constexpr int VJ = (PLANE + 16 * NT - 1) / (16 * NT);  // 16-byte pieces per thread of a V tile
+  constexpr bool VJ_PART = PLANE % (16 * NT) != 0;       // the last piece: the first threads only
   // loads issued after V(kt+2) that may still be in flight when this wave's
   // K(kt+2) and V(kt+2) must have landed (end of step kt): the K/V loads of
   // the NKS-2 later steps
   constexpr int VMW = (NKS - 2) * 2 * IPW;
   static_assert(NKS >= 3, "K/V tiles are issued at least three steps ahead");
 
-  __shared__ __align__(1024) char s_k[NKS * PLANE];
-  __shared__ __align__(1024) char s_v[NVS * PLANE];
+  // K ring, then V ring (the output tile reuses both once the last step is done)
+  __shared__ __align__(1024) char s_kv[(NKS + NVS) * PLANE];
+  __shared__ __align__(1024) char s_dummy[SPLIT ? 1024 : 16];   // target of the loads that read nothing
+  char *const s_k = s_kv;
+  char *const s_v = s_kv + NKS * PLANE;
   __shared__ int s_tab[kTabP];
 
   const int tid = threadIdx.x;
@@ -258,18 +286,28 @@ void prefill_pipe_kernel(PrefillParams p) {
   u32x4 qb[NCCR];  // loaded in the prologue
 
   // ---- loads ----
-  // K: wave w fills blocks w*IPW .. +IPW of a tile (chunk b / DQ, dims 32 (b % DQ)..)
-  const int kb0 = w * IPW;
-  const int k_chunk = kb0 / DQ;
+  // K: wave w fills blocks kb0 .. kb0 + nblk - 1 of a tile (block b: chunk
+  // b / DQ, dims 32 (b % DQ)..)
+  const int k_chunk = SPLIT ? w >> 1 : w * IPW / DQ;
+  const int kq0 = SPLIT ? 3 * (w & 1) : w * IPW % DQ;   // first block within the chunk
+  const int kb0 = k_chunk * DQ + kq0;
+  const int nblk = SPLIT ? ((w & 1) ? DQ - 3 : 3) : IPW;
   // lanes whose 8 dims lie past the real head size load nothing (an offset
   // past every buffer resource reads as zero)
   // (the per-block offsets are held as scalars, not an array a lambda captures)
   auto k_off = [&](int j) {
-    const int d0 = 32 * (kb0 % DQ + j) + 8 * (lane >> 4);
-    return d0 < DR ? 2u * ((lane & 15) * DR + d0) : 0x80000000u;
+    const int d0 = 32 * (kq0 + j) + 8 * (lane >> 4);
+    return d0 < DR && j < nblk ? 2u * ((lane & 15) * DR + d0) : 0x80000000u;
   };
-  const unsigned k_dma0 = k_off(0), k_dma1 = DR == D || IPW < 2 ? 0u : k_off(1),
-                 k_dma2 = DR == D || IPW < 3 ? 0u : k_off(2), k_dma3 = DR == D || IPW < 4 ? 0u : k_off(3);
+  constexpr bool DMA_IMM = DR == D && !SPLIT;   // block j at immediate offset 64 j of one lane offset
+  const unsigned k_dma0 = k_off(0), k_dma1 = DMA_IMM || IPW < 2 ? 0u : k_off(1),
+                 k_dma2 = DMA_IMM || IPW < 3 ? 0u : k_off(2), k_dma3 = DMA_IMM || IPW < 4 ? 0u : k_off(3);
+  // LDS destination of load j within a tile slot (a scratch block for a load
+  // that reads nothing)
+  auto dma_dst = [&](char *slot, int j) __attribute__((always_inline)) -> char * {
+    if constexpr (SPLIT) return j < nblk ? slot + (kb0 + j) * 1024 : s_dummy;
+    return slot + (kb0 + j) * 1024;
+  };
   // Page of one 16-key chunk of tile kt (-1: none, or past the last tile).
   // The lookups for a step's loads are read from LDS during the previous
   // step, so that no step starts by waiting for one.
@@ -290,14 +328,14 @@ void prefill_pipe_kernel(PrefillParams p) {
   };
   auto issue_k = [&](int kt, int phys) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(p.k, kt, k_chunk, phys);
-    char *dst = s_k + ((kt - kt_first) % NKS) * PLANE + kb0 * 1024;
+    char *slot = s_k + ((kt - kt_first) % NKS) * PLANE;
 #pragma unroll
     for (int j = 0; j < IPW; ++j)
-      if constexpr (DR == D)   // block j is 32 dims (64 bytes) further along the row
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(dst + j * 1024), 16, k_dma0, 64 * j, 0, 0);
+      if constexpr (DMA_IMM)   // block j is 32 dims (64 bytes) further along the row
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)dma_dst(slot, j), 16, k_dma0, 64 * j, 0, 0);
       else
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rs, (lds_void *)(dst + j * 1024), 16, j == 0 ? k_dma0 : j == 1 ? k_dma1 : j == 2 ? k_dma2 : k_dma3, 0, 0,
+            rs, (lds_void *)dma_dst(slot, j), 16, j == 0 ? k_dma0 : j == 1 ? k_dma1 : j == 2 ? k_dma2 : k_dma3, 0, 0,
             0);
   };
   // V: blocks (chunk, md) of 1 KiB, the same chunk as K; DMA lane m of block
@@ -305,25 +343,24 @@ void prefill_pipe_kernel(PrefillParams p) {
   // [8q8 ..+8], q8 = 4md + 2(((m%32)/8)%2) + m%2: the two 8-byte pieces that
   // the transposing read of region (c, md, half m/32) hands lanes 2(m%32)
   // and 2(m%32)+1.  bf16 tiles are converted to fp16 in place afterwards.
-  const int vb0 = w * IPW;
   auto v_off = [&](int j) {
     const int m = lane & 31;
     const int key = 8 * (lane >> 5) + 4 * (m >> 4) + ((m >> 1) & 3);
-    const int q8 = 4 * (vb0 % MD + j) + 2 * ((m >> 3) & 1) + (m & 1);
-    return 8 * q8 < DR ? (unsigned)(key * DR * 2 + 16 * q8) : 0x80000000u;
+    const int q8 = 4 * (kq0 + j) + 2 * ((m >> 3) & 1) + (m & 1);
+    return 8 * q8 < DR && j < nblk ? (unsigned)(key * DR * 2 + 16 * q8) : 0x80000000u;
   };
-  const unsigned v_dma0 = v_off(0), v_dma1 = DR == D || IPW < 2 ? 0u : v_off(1),
-                 v_dma2 = DR == D || IPW < 3 ? 0u : v_off(2), v_dma3 = DR == D || IPW < 4 ? 0u : v_off(3);
+  const unsigned v_dma0 = v_off(0), v_dma1 = DMA_IMM || IPW < 2 ? 0u : v_off(1),
+                 v_dma2 = DMA_IMM || IPW < 3 ? 0u : v_off(2), v_dma3 = DMA_IMM || IPW < 4 ? 0u : v_off(3);
   auto issue_v = [&](int kt, int phys) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(p.v, kt, k_chunk, phys);
-    char *dst = s_v + ((kt - kt_first) % NVS) * PLANE + vb0 * 1024;
+    char *slot = s_v + ((kt - kt_first) % NVS) * PLANE;
 #pragma unroll
     for (int j = 0; j < IPW; ++j)
-      if constexpr (DR == D)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(dst + j * 1024), 16, v_dma0, 64 * j, 0, 0);
+      if constexpr (DMA_IMM)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)dma_dst(slot, j), 16, v_dma0, 64 * j, 0, 0);
       else
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rs, (lds_void *)(dst + j * 1024), 16, j == 0 ? v_dma0 : j == 1 ? v_dma1 : j == 2 ? v_dma2 : v_dma3, 0, 0,
+            rs, (lds_void *)dma_dst(slot, j), 16, j == 0 ? v_dma0 : j == 1 ? v_dma1 : j == 2 ? v_dma2 : v_dma3, 0, 0,
             0);
   };
   const unsigned v_base = lds_addr(s_v);
@@ -333,7 +370,8 @@ void prefill_pipe_kernel(PrefillParams p) {
     if constexpr (DT == DD_BF16) {
       const unsigned base = v_base + ((kt - kt_first) % NVS) * PLANE + 16u * tid;
 #pragma unroll
-      for (int j = 0; j < VJ; ++j) x[j] = lds_read128(base, j * 16 * NT);
+      for (int j = 0; j < VJ; ++j)
+        if (!VJ_PART || j + 1 < VJ || 16 * (tid + j * NT) < PLANE) x[j] = lds_read128(base, j * 16 * NT);
     }
   };
   auto convert_v_write = [&](int kt, u32x4 (&x)[VJ]) __attribute__((always_inline)) {
@@ -342,7 +380,8 @@ void prefill_pipe_kernel(PrefillParams p) {
 #pragma unroll
       for (int j = 0; j < VJ; ++j) lgkm_wait(x[j], 0);
 #pragma unroll
-      for (int j = 0; j < VJ; ++j) lds_write128(base, j * 16 * NT, bf16x8_to_f16x8(x[j]));
+      for (int j = 0; j < VJ; ++j)
+        if (!VJ_PART || j + 1 < VJ || 16 * (tid + j * NT) < PLANE) lds_write128(base, j * 16 * NT, bf16x8_to_f16x8(x[j]));
     }
   };
   auto convert_v = [&](int kt) __attribute__((always_inline)) {
@@ -441,7 +480,7 @@ void prefill_pipe_kernel(PrefillParams p) {
   auto mfma_phase = [&](auto has_next_c, int kt, f32x16 (&s)[NSB], const u32x4 (&pp)[NSB][2], auto &&loads)
       __attribute__((always_inline)) {
     constexpr bool HN = decltype(has_next_c)::value;
-    constexpr int NS = HN ? NSB * NCCR : 0, NV = 2 * NSB * MDR, N = NS + NV, R = DD_PF_RING;
+    constexpr int NS = HN ? NSB * NCCR : 0, NV = 2 * NSB * MDR, N = NS + NV, R = pipe_ring<D>();
     const unsigned kb_addr = k_rd + (unsigned)(((kt + 1 - kt_first) % NKS) * PLANE);
     const unsigned vb = v_rd + (unsigned)(((kt - kt_first) % NVS) * PLANE);
     // operand i < NS: one K read; else two transposing reads
@@ -640,13 +679,14 @@ void prefill_pipe_kernel(PrefillParams p) {
   // pieces of contiguous (query row, head) rows: stored straight from the
   // O^T registers, each 8-byte store instruction would touch 32 rows.  Each
   // wave writes its 32 normalised columns as rows (padded by 16 bytes) into
-  // the V ring, free once every wave has finished its last P.V reads and
-  // its loads -- the zero-size trailing ones included -- have landed.
+  // the V ring (the 160 layout: from the start of the K ring on), free once
+  // every wave has finished its last P.V reads and its loads -- the
+  // zero-size trailing ones included -- have landed.
   lgkm_drain();
   barrier();
   constexpr int ORS = 2 * DR + 16;      // LDS row stride of the output tile
-  static_assert(NW * 32 * ORS <= NVS * PLANE, "output tile fits the V ring");
-  char *otile = s_v + w * 32 * ORS;
+  static_assert(NW * 32 * ORS <= (NKS + NVS) * PLANE, "output tile fits the K and V rings");
+  char *otile = (NW * 32 * ORS <= NVS * PLANE ? s_v : s_kv) + w * 32 * ORS;
   if (colok) {
     const float inv = 1.f / l;
 #pragma unroll
@@ -701,8 +741,8 @@ int pipe_dims(const PrefillParams &p, int dim, int max_len, int plan_len, hipStr
     case 96: return launch_pipe<DT, 128, 96>(p, max_len, plan_len, s);
     case 112: return launch_pipe<DT, 128, 112>(p, max_len, plan_len, s);
     case 128: return launch_pipe<DT, 128>(p, max_len, plan_len, s);
-    case 144: return launch_pipe<DT, 256, 144>(p, max_len, plan_len, s);
-    case 160: return launch_pipe<DT, 256, 160>(p, max_len, plan_len, s);
+    case 144: return launch_pipe<DT, 160, 144>(p, max_len, plan_len, s);
+    case 160: return launch_pipe<DT, 160>(p, max_len, plan_len, s);
     case 176: return launch_pipe<DT, 256, 176>(p, max_len, plan_len, s);
     case 192: return launch_pipe<DT, 256, 192>(p, max_len, plan_len, s);
     case 208: return launch_pipe<DT, 256, 208>(p, max_len, plan_len, s);

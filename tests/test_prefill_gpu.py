@@ -179,18 +179,20 @@ def test_prefill_other_head_sizes(dtype, dim):
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize('dim', [144, 160, 176, 192, 208, 224, 240])
 def test_prefill_wide_head_sizes(dtype, dim):
-    """Head sizes between 128 and 256 on the 16-bit kernel's 256 layout (rows
-    of the real length; the dims past it are zeros the MFMAs skip)."""
+    """Head sizes between 128 and 256 on the 16-bit kernel's 160 and 256
+    layouts (rows of the real length; the dims past it are zeros the MFMAs
+    skip)."""
     out, exp = run_segments([3, 64, 100], [0, 200, 17], 12, 4, dim, dtype, seed=dim)
     check(out, exp)
 
 
-@pytest.mark.parametrize('dim', [160, 224, 256])
+@pytest.mark.parametrize('dim', [144, 160, 224, 256])
 @pytest.mark.parametrize('page,window,heads,kvh', [(16, 0, 32, 8), (32, 70, 8, 1), (16, 0, 40, 2),
                                                    (16, 300, 130, 1)])
 def test_prefill_wide_head_sizes_pages_windows(dim, page, window, heads, kvh):
-    """The 256 layout with larger pages, windows, wide groups, and more query
-    heads per KV head than its 128-column work item (130: the exact kernel)."""
+    """The 160 and 256 layouts with larger pages, windows, wide groups, and
+    130 query heads per KV head (at 224 and 256 more than the 128-column work
+    item: the exact kernel)."""
     lengths = [1, 77, 200] if heads <= 40 else [1, 9, 40]
     starts = [5, 0, 1500] if heads <= 40 else [0, 17, 100]
     out, exp = run_segments(lengths, starts, heads, kvh, dim, torch.bfloat16, seed=dim + page + window + heads,

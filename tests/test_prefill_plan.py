@@ -86,13 +86,16 @@ def test_plan_rejects_bad_arguments():
     with pytest.raises(Exception):
         ragged.prefill_plan([4], [0], 8, 2, 152)     # no 16-bit MFMA kernel for head dim 152
     with pytest.raises(Exception):
-        ragged.prefill_plan([4], [0], 130, 1, 160)   # more heads per KV head than an item's 128 columns
+        ragged.prefill_plan([4], [0], 130, 1, 224)   # more heads per KV head than an item's 128 columns
     assert len(ragged.prefill_plan([], [], 8, 2, 128)) == 0
     cols, kt = ctypes.c_int(), ctypes.c_int()
     assert _native.library().dd_prefill_geometry(152, ctypes.byref(cols), ctypes.byref(kt)) != 0
     assert _native.library().dd_prefill_geometry(16, ctypes.byref(cols), ctypes.byref(kt)) != 0
-    # the 256 layout takes the multiples of 16 above 128
-    for dim in (144, 160, 240, 256):
+    # the 160 layout takes 144 and 160, the 256 layout the multiples of 16 above
+    for dim in (144, 160):
+        assert _native.library().dd_prefill_geometry(dim, ctypes.byref(cols), ctypes.byref(kt)) == 0
+        assert (cols.value, kt.value) == (256, 64)
+    for dim in (176, 240, 256):
         assert _native.library().dd_prefill_geometry(dim, ctypes.byref(cols), ctypes.byref(kt)) == 0
         assert (cols.value, kt.value) == (128, 32)
 
