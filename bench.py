@@ -312,8 +312,8 @@ def bench_mixed(args, dev, dtype=torch.bfloat16):
     n_chunks = sum(1 for n in lengths if n > 1)
     t_prefill = sum(lengths[:n_chunks])
     flops = 4 * 32 * D * sum(n * s + n * (n + 1) // 2 for n, s in zip(lengths[:n_chunks], starts[:n_chunks]))
-    # the decode kernels take power-of-two head sizes (and 96), as the
-    # reference's Triton decode does; at other sizes only the prefill runs
+    # decode rows where a streamed decode kernel exists (head sizes 64, 96,
+    # 128, 256); at other head sizes the line times the prefill only
     decode_rows = D in (64, 96, 128, 256)
 
     def step(ev=None):

@@ -70,6 +70,7 @@ static int decode_entry(int phase, const void *q, int q_dtype, const void *k, co
   p.H = heads;
   p.KH = kv_heads;
   p.G = heads / kv_heads;
+  p.DR = dim;
   p.gsub = 1;
   p.table_w = table_width;
   p.table_rows = table_rows;

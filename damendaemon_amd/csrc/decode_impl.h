@@ -45,6 +45,7 @@ struct DecodeParams {
   const float *sinks;
   long capacity;  // pages (paged) or slots (slotted); guards addressing
   int B, H, KH, G;
+  int DR;         // head size: row length of Q, K, V, the output and the partials
   int gsub;       // workgroups per (sequence, KV head): query heads in groups of <= 16
   int table_w, table_rows;
   int page;       // page_size (paged) or context (slotted)
@@ -188,6 +189,11 @@ __global__ __launch_bounds__(256) DD_DECODE_ATTR void decode_kernel(DecodeParams
   constexpr int NC4 = D / 16;                                       // fp32 k-chunks
   constexpr int KB = KVT == DD_F32 ? 4 : (KVT == DD_I8 ? 1 : 2);    // bytes per element
   constexpr int PD = KVT == DD_I8 ? DD_DECODE_PD_I8 : DD_DECODE_PD;  // pages in flight per wave
+  // The real head size DR (a multiple of 16, at most D) sets every row
+  // stride; the dims DR .. D-1 of the layout hold zero queries (so the K
+  // bytes read for them, a clamped copy of the row's first dims, add
+  // nothing) and V columns that are never stored.
+  const int DR = p.DR;
 
   __shared__ float s_p[kWaves][16][GB];       // per-wave page probabilities
   __shared__ float s_o[GB][D];                // cross-wave output accumulator
@@ -236,15 +242,16 @@ __global__ __launch_bounds__(256) DD_DECODE_ATTR void decode_kernel(DecodeParams
     const unsigned short *qb = (const unsigned short *)p.q;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      if (tl < G) {
-        qa[c] = *(const u32x4 *)(qb + (head0 + tl) * D + 8 * r + 32 * c);
+      if (tl < G && 8 * r + 32 * c < DR) {
+        qa[c] = *(const u32x4 *)(qb + (head0 + tl) * DR + 8 * r + 32 * c);
       } else {
         qa[c] = u32x4{0, 0, 0, 0};
       }
     }
   } else {
     for (int i = threadIdx.x; i < G * D; i += 256) {
-      s_q[i / D][i % D] = load_as<QT>(p.q, head0 * D + i);
+      const int d = i % D;
+      s_q[i / D][d] = d < DR ? load_as<QT>(p.q, (head0 + i / D) * DR + d) : 0.f;
     }
     __syncthreads();
   }
@@ -266,6 +273,7 @@ __global__ __launch_bounds__(256) DD_DECODE_ATTR void decode_kernel(DecodeParams
   const char *vbytes = (const char *)p.v;
   const int vtok_lane = lane / LPT;        // token within a V load
   const int vdim = VE * (lane % LPT);      // first dim of this lane's V slice
+  const int vdim_ld = vdim < DR ? vdim : 0;  // (a lane past DR reads the row's first dims)
   const bool v_lane_on = lane < LPT * TPI;
 
   // Registers of one page: raw K (MFMA layout), raw V (VALU layout) and,
@@ -287,7 +295,7 @@ __global__ __launch_bounds__(256) DD_DECODE_ATTR void decode_kernel(DecodeParams
   // Per-lane byte offsets inside a 16-token chunk are loop invariant; the
   // chunk base is wave-uniform, so each load is SGPR base + 32-bit offset.
   auto load_page = [&](int pg, PageRegs &R) {
-    const long base = chunk_base(p, row, kh, pg, D);
+    const long base = chunk_base(p, row, kh, pg, DR);
     R.base = base;
     const long sb = base < 0 ? 0 : base;
     const int lim = p.paged ? 15 : min(15, p.page - 1 - pg * 16);
@@ -296,24 +304,34 @@ __global__ __launch_bounds__(256) DD_DECODE_ATTR void decode_kernel(DecodeParams
     const char *vb = vbytes + KB * sb;
     if constexpr (KVT == DD_I8) {
 #pragma unroll
-      for (int c = 0; c < NC; ++c) R.k8[c] = __builtin_nontemporal_load((const u32x2 *)(kb + (krow * D + 8 * r + 32 * c)));
-      const unsigned short *ksc = p.ks + (sb / D) * p.ngroups;
+      for (int c = 0; c < NC; ++c) {
+        const int d0 = 8 * r + 32 * c < DR ? 8 * r + 32 * c : 0;
+        R.k8[c] = __builtin_nontemporal_load((const u32x2 *)(kb + (krow * DR + d0)));
+      }
+      const unsigned short *ksc = p.ks + (sb / DR) * p.ngroups;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        R.ks[c] = (c == 0 || p.group != D) ? half_bits_to_float(ksc[krow * p.ngroups + (32 * c) / p.group]) : 0.f;
+        R.ks[c] = (32 * c < DR && (c == 0 || p.group != DR)) ? half_bits_to_float(ksc[krow * p.ngroups + (32 * c) / p.group])
+                                                             : 0.f;
       }
     } else if constexpr (kMfma) {
 #pragma unroll
-      for (int c = 0; c < NC; ++c) R.k[c] = __builtin_nontemporal_load((const u32x4 *)(kb + 2u * (krow * D + 8 * r + 32 * c)));
+      for (int c = 0; c < NC; ++c) {
+        const int d0 = 8 * r + 32 * c < DR ? 8 * r + 32 * c : 0;
+        R.k[c] = __builtin_nontemporal_load((const u32x4 *)(kb + 2u * (krow * DR + d0)));
+      }
     } else {
 #pragma unroll
-      for (int c = 0; c < NC4; ++c) R.k[c] = __builtin_nontemporal_load((const u32x4 *)(kb + 4u * (krow * D + 4 * r + 16 * c)));
+      for (int c = 0; c < NC4; ++c) {
+        const int d0 = 4 * r + 16 * c < DR ? 4 * r + 16 * c : 0;
+        R.k[c] = __builtin_nontemporal_load((const u32x4 *)(kb + 4u * (krow * DR + d0)));
+      }
     }
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
       const unsigned vrow = (unsigned)min(it * TPI + vtok_lane, lim);
-      R.v[it] = __builtin_nontemporal_load((const u32x4 *)(vb + KB * (vrow * D + vdim)));
-      if constexpr (KVT == DD_I8) R.vs[it] = half_bits_to_float(p.vs[(sb / D) * p.ngroups + vrow * p.ngroups + vdim / p.group]);
+      R.v[it] = __builtin_nontemporal_load((const u32x4 *)(vb + KB * (vrow * DR + vdim_ld)));
+      if constexpr (KVT == DD_I8) R.vs[it] = half_bits_to_float(p.vs[(sb / DR) * p.ngroups + vrow * p.ngroups + vdim_ld / p.group]);
     }
   };
 
@@ -340,7 +358,7 @@ __global__ __launch_bounds__(256) DD_DECODE_ATTR void decode_kernel(DecodeParams
     // -- logits: lane holds token tl for heads 4r+i --
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
     if constexpr (KVT == DD_I8) {
-      if (p.group == D) {
+      if (p.group == DR) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) s = mfma16x16x32<QT>(qa[c], widen_i8x8<QT>(cur.k8[c]), s);
 #pragma unroll
@@ -567,9 +585,9 @@ __global__ __launch_bounds__(256) DD_DECODE_ATTR void decode_kernel(DecodeParams
     __syncthreads();
   }
 
-  for (int i = threadIdx.x; i < G * D; i += 256) {
-    const int h = i / D;
-    const int d = i % D;
+  for (int i = threadIdx.x; i < G * DR; i += 256) {
+    const int h = i / DR;
+    const int d = i - h * DR;
     float mm = s_ml[0][0][h];
     for (int ww = 1; ww < kWaves; ++ww) mm = fmaxf(mm, s_ml[ww][0][h]);
     float l = 0.f;
@@ -587,9 +605,9 @@ __global__ __launch_bounds__(256) DD_DECODE_ATTR void decode_kernel(DecodeParams
         l = l * f + fast_exp2(sk - m2);
         o *= f;
       }
-      store_as<QT>(p.out, bh * D + d, o / l);
+      store_as<QT>(p.out, bh * DR + d, o / l);
     } else {
-      p.part[(bh * p.splits + split) * D + d] = o / l;
+      p.part[(bh * p.splits + split) * DR + d] = o / l;
       if (d == 0) p.lse[bh * p.splits + split] = mm + log2f(l);
     }
   }
@@ -660,8 +678,8 @@ int launch_decode(const DecodeParams &p, hipStream_t stream, int phase) {
     DD_LAUNCH_CHECK();
   }
   if ((phase & 2) && p.splits > 1) {
-    hipLaunchKernelGGL((merge_kernel<QT>), dim3((unsigned)((long)p.B * p.H)), dim3(D < 256 ? D : 256), 0,
-                       stream, p, D);
+    hipLaunchKernelGGL((merge_kernel<QT>), dim3((unsigned)((long)p.B * p.H)), dim3(p.DR < 256 ? p.DR : 256), 0,
+                       stream, p, p.DR);
     DD_LAUNCH_CHECK();
   }
   return DD_OK;
@@ -692,8 +710,9 @@ namespace dd_decode {
 // Instantiated once per dtype pair in decode_<dtype>.hip.  bf16 / f16 / fp32
 // pages at D = 64, 96, 128, 256 and int8 pages with one scale per row or per
 // 32 channels at D = 64, 128, 256 take the streamed kernels (decode_stream.h),
-// any number of query heads per KV head; int8 at D = 96 and other int8
-// groupings take decode_kernel.
+// any number of query heads per KV head; int8 at D = 96, other int8
+// groupings and every other head size that is a multiple of 16 up to 256
+// take decode_kernel.
 template <int KVT, int QT>
 int dispatch_d(const DecodeParams &p0, int D, hipStream_t s, int phase) {
   // streamed kernels: more than 16 query heads per KV head run as gsub
@@ -741,13 +760,13 @@ int dispatch_d(const DecodeParams &p0, int D, hipStream_t s, int phase) {
       }
     }
   }
-  switch (D) {
-    case 64: return dispatch_g<KVT, QT, 64>(p0, s, phase);
-    case 96: return dispatch_g<KVT, QT, 96>(p0, s, phase);
-    case 128: return dispatch_g<KVT, QT, 128>(p0, s, phase);
-    case 256: return dispatch_g<KVT, QT, 256>(p0, s, phase);
-    default: return DD_EUNSUPPORTED;
-  }
+  // the general kernel: the smallest layout of 64, 96, 128, 256 dims that
+  // holds the head size (a multiple of 16)
+  if (D <= 0 || D % 16 || D > 256) return DD_EUNSUPPORTED;
+  if (D <= 64) return dispatch_g<KVT, QT, 64>(p0, s, phase);
+  if (D <= 96) return dispatch_g<KVT, QT, 96>(p0, s, phase);
+  if (D <= 128) return dispatch_g<KVT, QT, 128>(p0, s, phase);
+  return dispatch_g<KVT, QT, 256>(p0, s, phase);
 }
 
 }  // namespace dd_decode

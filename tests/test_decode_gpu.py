@@ -224,6 +224,41 @@ def test_int8_nan_scales_and_expired_rows(dim, group, window):
     check(run_case(case, window=window), expected, torch.int8)
 
 
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize('dim', [16, 32, 48, 80, 112, 144, 160, 192, 240])
+def test_other_head_sizes(dtype, dim):
+    """Head sizes (multiples of 16) without a streamed kernel: the general kernel's smallest
+    layout that holds them (64, 96, 128 or 256 dims), rows of the real length; NaN-filled
+    pools, several splits, 4 query heads per KV head, with and without a window."""
+    contexts = [1, 17, 300, 2100]
+    case = paged_decode_case(contexts, 12, 3, dim, dtype, seed=dim, nan_fill=True)
+    check(run_case(case), oracle_case(case), dtype)
+    check(run_case(case, window=45), oracle_case(case, window=45), dtype)
+
+
+@pytest.mark.parametrize('dim,group', [(48, 48), (80, 80), (160, 160), (160, 32), (192, 32), (224, 224)])
+def test_int8_other_head_sizes(dim, group):
+    """Q8 pages at head sizes without a streamed kernel, NaN scales on unused rows."""
+    contexts = [1, 15, 17, 300, 1111]
+    case = paged_decode_case(contexts, 12, 3, dim, torch.float32, seed=dim + group, nan_fill=True)
+    qk, ks = oracle.quantize_q8(case['cache_k'], group)
+    qv, vs = oracle.quantize_q8(case['cache_v'], group)
+    expected = oracle.decode_attention(case['query'].to(torch.bfloat16), qk, qv, case['positions'], case['slots'],
+                                       page_table=case['page_table'], k_scale=ks, v_scale=vs)
+    ks[~torch.isfinite(ks)] = float('nan')
+    vs[~torch.isfinite(vs)] = float('nan')
+    case.update(cache_k=qk, cache_v=qv, k_scale=ks, v_scale=vs, query=case['query'].to(torch.bfloat16))
+    check(run_case(case), expected, torch.int8)
+
+
+def test_unsupported_head_size_refused():
+    """A head size that is not a multiple of 16 (or above 256) is refused before any launch."""
+    for dim in (72, 272):
+        case = paged_decode_case([5, 40], 4, 2, dim, torch.bfloat16, seed=dim)
+        with pytest.raises(Exception, match='unsupported'):
+            run_case(case)
+
+
 @pytest.mark.parametrize('page', [32, 64])
 @pytest.mark.parametrize('kind', ['bf16', 'int8'])
 def test_larger_pages(page, kind):
