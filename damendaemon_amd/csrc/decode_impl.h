@@ -189,7 +189,7 @@ __global__ __launch_bounds__(256) DD_DECODE_ATTR void decode_kernel(DecodeParams
   constexpr int NC4 = D / 16;                                       // fp32 k-chunks
   constexpr int KB = KVT == DD_F32 ? 4 : (KVT == DD_I8 ? 1 : 2);    // bytes per element
   constexpr int PD = KVT == DD_I8 ? DD_DECODE_PD_I8 : DD_DECODE_PD;  // pages in flight per wave
-  // The real head size DR (a multiple of 16, at most D) sets every row
+  // The real head size DR (a multiple of 8, of 16 for int8; at most D) sets every row
   // stride; the dims DR .. D-1 of the layout hold zero queries (so the K
   // bytes read for them, a clamped copy of the row's first dims, add
   // nothing) and V columns that are never stored.
@@ -711,8 +711,8 @@ namespace dd_decode {
 // pages at D = 64, 96, 128, 256 and int8 pages with one scale per row or per
 // 32 channels at D = 64, 128, 256 take the streamed kernels (decode_stream.h),
 // any number of query heads per KV head; int8 at D = 96, other int8
-// groupings and every other head size that is a multiple of 16 up to 256
-// take decode_kernel.
+// groupings and every other head size up to 256 that is a multiple of 8 (16
+// for int8 pages) take decode_kernel.
 template <int KVT, int QT>
 int dispatch_d(const DecodeParams &p0, int D, hipStream_t s, int phase) {
   // streamed kernels: more than 16 query heads per KV head run as gsub
@@ -761,8 +761,9 @@ int dispatch_d(const DecodeParams &p0, int D, hipStream_t s, int phase) {
     }
   }
   // the general kernel: the smallest layout of 64, 96, 128, 256 dims that
-  // holds the head size (a multiple of 16)
-  if (D <= 0 || D % 16 || D > 256) return DD_EUNSUPPORTED;
+  // holds the head size (a multiple of 8, of 16 for int8 pages: whole
+  // 16-byte loads)
+  if (D <= 0 || D % (KVT == DD_I8 ? 16 : 8) || D > 256) return DD_EUNSUPPORTED;
   if (D <= 64) return dispatch_g<KVT, QT, 64>(p0, s, phase);
   if (D <= 96) return dispatch_g<KVT, QT, 96>(p0, s, phase);
   if (D <= 128) return dispatch_g<KVT, QT, 128>(p0, s, phase);

@@ -225,9 +225,9 @@ def test_int8_nan_scales_and_expired_rows(dim, group, window):
 
 
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize('dim', [16, 32, 48, 80, 112, 144, 160, 192, 240])
+@pytest.mark.parametrize('dim', [8, 16, 24, 32, 40, 48, 72, 80, 112, 144, 160, 192, 200, 240])
 def test_other_head_sizes(dtype, dim):
-    """Head sizes (multiples of 16) without a streamed kernel: the general kernel's smallest
+    """Head sizes (multiples of 8) without a streamed kernel: the general kernel's smallest
     layout that holds them (64, 96, 128 or 256 dims), rows of the real length; NaN-filled
     pools, several splits, 4 query heads per KV head, with and without a window."""
     contexts = [1, 17, 300, 2100]
@@ -252,8 +252,8 @@ def test_int8_other_head_sizes(dim, group):
 
 
 def test_unsupported_head_size_refused():
-    """A head size that is not a multiple of 16 (or above 256) is refused before any launch."""
-    for dim in (72, 272):
+    """A head size that is not a multiple of 8 (or above 256) is refused before any launch."""
+    for dim in (36, 272):
         case = paged_decode_case([5, 40], 4, 2, dim, torch.bfloat16, seed=dim)
         with pytest.raises(Exception, match='unsupported'):
             run_case(case)
