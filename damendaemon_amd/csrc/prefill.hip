@@ -32,9 +32,10 @@ struct Geometry {
   int cols, kt;
 };
 // prefill_pipe_kernel's layouts: 8 waves x 32 columns and 64-key tiles for
-// the 64, 128 and 160 layouts, 4 waves x 32 columns and 32-key tiles for the
-// 256 layout (prefill_pipe.hip: pipe_waves, pipe_keys).
-constexpr Geometry kGeom64{256, 64};
+// the 128 and 160 layouts (128-key tiles for the 64 layout), 4 waves x 32
+// columns and 32-key tiles for the 256 layout (prefill_pipe.hip:
+// pipe_waves, pipe_keys).
+constexpr Geometry kGeom64{256, 128};
 constexpr Geometry kGeom128{256, 64};
 constexpr Geometry kGeom160{256, 64};
 constexpr Geometry kGeom256{128, 32};
