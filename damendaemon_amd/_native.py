@@ -17,7 +17,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 LIBRARY = Path(__file__).resolve().parent / '_lib' / 'libdamendaemon_amd.so'
 
 F32, F16, BF16, I8 = 0, 1, 2, 3
@@ -29,6 +29,7 @@ _p, _i, _i64, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 SIGNATURES = {
     'dd_abi_version': [],
     'dd_decode_splits': [_i, _i, ctypes.POINTER(_i)],
+    'dd_decode_splits_for': [_i, _i, _i, _i, ctypes.POINTER(_i)],
     'dd_decode_attention': [_p, _i, _p, _p, _i, _p, _p, _i,   # q .. group
                             _p, _p, _p, _i, _i,               # positions, slots, table, rows, width
                             _i, _i, _i, _i, _i, _i64, _i, _f,  # B H KH D page cap window scale

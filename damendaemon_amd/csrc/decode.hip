@@ -39,6 +39,24 @@ extern "C" int dd_decode_splits(int max_context, int batch_kv, int *split_tokens
   return (int)dd_cdiv(max_context, st);
 }
 
+extern "C" int dd_decode_splits_for(int max_context, int batch_kv, int dim, int kv_dtype, int *split_tokens) {
+  int st = 0;
+  const int n = dd_decode_splits(max_context, batch_kv, &st);
+  if (n <= 0) return n;
+  // Measured on 64 sequences of U[512, 8192] keys at D = 256, bf16: 4 KV
+  // heads 198 us with 1,024-key splits vs 215 us with 1,408; 8 KV heads 346
+  // vs 354 us (not capped by this rule); 16 x 32768 keys on 2 KV heads keeps
+  // its 2,048 (178 us vs 189 us with 1,024).
+  constexpr long kSlots = 2L * 256;   // resident workgroups of the D = 256 kernel
+  if (dim == 256 && (kv_dtype == DD_BF16 || kv_dtype == DD_F16) && batch_kv >= 128 &&
+      (long)batch_kv * n < 4 * kSlots && st > 1024) {
+    if (split_tokens) *split_tokens = 1024;
+    return (int)dd_cdiv(max_context, 1024);
+  }
+  if (split_tokens) *split_tokens = st;
+  return n;
+}
+
 static int decode_entry(int phase, const void *q, int q_dtype, const void *k, const void *v, int kv_dtype,
                                    const void *k_scale, const void *v_scale, int group,
                                    const int64_t *positions, const int64_t *slots, const int32_t *page_table,

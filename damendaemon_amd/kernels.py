@@ -16,9 +16,10 @@ from . import _native
 from ._native import DTYPE_CODES, call, ptr
 
 
-def _splits(max_context, batch_kv):
-    """Split count and tokens per split: the library's policy, or a fixed
-    split size from DAMENDAEMON_AMD_SPLIT_TOKENS (a multiple of 64; tuning)."""
+def _splits(max_context, batch_kv, dim, kv_dtype):
+    """Split count and tokens per split: the library's policy for this head
+    size and page dtype, or a fixed split size from
+    DAMENDAEMON_AMD_SPLIT_TOKENS (a multiple of 64; tuning)."""
     forced = os.environ.get('DAMENDAEMON_AMD_SPLIT_TOKENS')
     if forced:
         tokens = int(forced)
@@ -26,7 +27,8 @@ def _splits(max_context, batch_kv):
             raise ValueError('DAMENDAEMON_AMD_SPLIT_TOKENS must be a positive multiple of 64')
         return -(-int(max_context) // tokens), tokens
     tokens = ctypes.c_int(0)
-    splits = _native.library().dd_decode_splits(int(max_context), int(batch_kv), ctypes.byref(tokens))
+    splits = _native.library().dd_decode_splits_for(int(max_context), int(batch_kv), int(dim), DTYPE_CODES[kv_dtype],
+                                                     ctypes.byref(tokens))
     if splits <= 0:
         raise ValueError('invalid decode geometry')
     return splits, tokens.value
@@ -51,7 +53,7 @@ def attention(query, cache_k, cache_v, positions, slots=None, window=0, scale=No
         from .attention_budget import query_rows
         batch, heads, _, dim = query.shape
         context = cache_k.shape[2] * (1 if page_table is None else page_table.shape[1])
-        splits, _ = _splits(context, batch * cache_k.shape[1])
+        splits, _ = _splits(context, batch * cache_k.shape[1], dim, cache_k.dtype)
         rows = query_rows(heads, dim, splits, scratch_bytes, query.element_size())
         if batch > rows:
             # Partition only independent query rows (kernels.py:237-252); each
@@ -123,7 +125,7 @@ def prepare_attention(query, cache_k, cache_v, positions, slots=None, window=0, 
         context = page_table.shape[1] * page_size
     else:
         context = page_size
-    splits, split_tokens = _splits(context, batch * kv_heads)
+    splits, split_tokens = _splits(context, batch * kv_heads, dim, cache_k.dtype)
     return DecodeLaunch(query, cache_k, cache_v, positions, slots, page_table, kv_heads, page_size, capacity,
                         group, k_scale, v_scale, window, scale, alibi, relative_bias, buckets,
                         relative_max_distance, sinks, splits, split_tokens, out)

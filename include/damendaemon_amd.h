@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define DD_ABI_VERSION 4
+#define DD_ABI_VERSION 5
 
 enum dd_dtype { DD_F32 = 0, DD_F16 = 1, DD_BF16 = 2, DD_I8 = 3 };
 
@@ -56,6 +56,17 @@ const char *dd_error_string(int code);
 int dd_decode_splits(int max_context, int batch_kv, int *split_tokens);
 
 /*
+ * The same policy for a given head size and page dtype (no counterpart in
+ * the reference, whose split choice ignores both): dd_decode_splits, except
+ * that at head size 256 with 16-bit pages, at least 128 (sequence, KV head)
+ * pairs and fewer than four splits per resident workgroup (2 per CU), splits
+ * hold at most 1,024 keys (that kernel's workgroups have two waves, so a
+ * longer split is a long unit of work that leaves CUs idle at the end).
+ * Same return values.
+ */
+int dd_decode_splits_for(int max_context, int batch_kv, int dim, int kv_dtype, int *split_tokens);
+
+/*
  * Ragged decode attention, one query row per sequence.
  * Replaces damendaemon/kernels.py:213-267 (`attention` with the `_attention`
  * and `_merge` Triton kernels), paged (page_table != NULL) or slotted.
@@ -82,7 +93,7 @@ int dd_decode_splits(int max_context, int batch_kv, int *split_tokens);
  *   out        (batch, heads, dim) q_dtype
  *   partial    fp32 (batch*heads, splits, dim)  scratch (unused if splits==1)
  *   lse        fp32 (batch*heads, splits)       scratch (unused if splits==1)
- *   splits, split_tokens  from dd_decode_splits()
+ *   splits, split_tokens  from dd_decode_splits() or dd_decode_splits_for()
  */
 int dd_decode_attention(const void *q, int q_dtype, const void *k,
                         const void *v, int kv_dtype, const void *k_scale,

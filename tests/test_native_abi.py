@@ -48,6 +48,38 @@ def test_split_policy_covers_context():
     assert lib.dd_decode_splits(0, 1, None) < 0
 
 
+def test_split_policy_for_head_size():
+    """The head-size-aware policy equals the plain one except at head size 256
+    with 16-bit pages, many (sequence, KV head) pairs and few splits per
+    resident workgroup, where splits hold at most 1,024 keys."""
+    from damendaemon_amd import _native
+    lib = _native.library()
+
+    def policy(ctx, bkh, dim, dtype):
+        tokens = ctypes.c_int()
+        splits = lib.dd_decode_splits_for(ctx, bkh, dim, dtype, ctypes.byref(tokens))
+        return splits, tokens.value
+
+    def plain(ctx, bkh):
+        tokens = ctypes.c_int()
+        splits = lib.dd_decode_splits(ctx, bkh, ctypes.byref(tokens))
+        return splits, tokens.value
+
+    assert policy(8192, 256, 256, _native.BF16) == (8, 1024)     # 64 sequences x 4 KV heads
+    assert policy(8192, 256, 256, _native.F16) == (8, 1024)
+    assert policy(8192, 512, 256, _native.BF16) == (6, 1408)     # 8 KV heads: six splits each, enough units
+    assert policy(32768, 32, 256, _native.BF16) == (16, 2048)    # C5
+    assert policy(8192, 512, 128, _native.BF16) == (6, 1408)     # C2
+    for ctx in (300, 1000, 4096, 8192, 32768):
+        for bkh in (1, 8, 100, 128, 300, 512, 4096):
+            for dim, dtype in ((64, _native.BF16), (128, _native.F32), (256, _native.F32), (256, _native.I8)):
+                assert policy(ctx, bkh, dim, dtype) == plain(ctx, bkh)
+            splits, st = policy(ctx, bkh, 256, _native.BF16)
+            assert st % 64 == 0 and 256 <= st <= plain(ctx, bkh)[1]
+            assert splits * st >= ctx > (splits - 1) * st
+    assert lib.dd_decode_splits_for(0, 1, 256, _native.BF16, None) < 0
+
+
 def test_split_policy_sizes_and_occupancy():
     """Split sizes are multiples of 64 in [256, 2048]; the tuned configurations keep
     theirs (64 x 8 KV heads over 8192-key tables: 1408; 16 x 2 over 32768: 2048); and
