@@ -83,14 +83,23 @@ typedef __attribute__((address_space(3))) void lds_void;
 #ifndef DD_STREAM_NW96
 #define DD_STREAM_NW96 8
 #endif
+// D = 64, 16-bit pages: 8 waves x 1 stage (C2 contexts, H32/KH8, bf16:
+// 93.5-93.9 us vs 99.0-102.8 us with 4 x 4; H64/KH8 97.5 vs 103-105 us).
 #ifndef DD_STREAM_NB64
-#define DD_STREAM_NB64 4
+#define DD_STREAM_NB64 1
+#endif
+#ifndef DD_STREAM_NW64
+#define DD_STREAM_NW64 8
+#endif
+// int8 pages at D = 64 (two chunks per step; its ring needs two stages)
+#ifndef DD_STREAM_I8_NB64
+#define DD_STREAM_I8_NB64 4
+#endif
+#ifndef DD_STREAM_I8_NW64
+#define DD_STREAM_I8_NW64 4
 #endif
 #ifndef DD_STREAM_NB256
 #define DD_STREAM_NB256 2
-#endif
-#ifndef DD_STREAM_NW64
-#define DD_STREAM_NW64 4
 #endif
 
 // f(integral_constant<int, I>) for I = 0 .. N-1, unrolled at compile time.
