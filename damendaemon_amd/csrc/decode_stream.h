@@ -91,9 +91,11 @@ typedef __attribute__((address_space(3))) void lds_void;
 #ifndef DD_STREAM_NW64
 #define DD_STREAM_NW64 8
 #endif
-// int8 pages at D = 64 (two chunks per step; its ring needs two stages)
+// int8 pages at D = 64 (two chunks per step; its ring needs two stages):
+// 4 waves x 2 stages (C2 contexts, H32/KH8: 60.1-60.6 us vs 75.4 us with 4 x 4;
+// 2 x 8 67-68, 3 x 4 66, 2 waves x 2 63-64 us)
 #ifndef DD_STREAM_I8_NB64
-#define DD_STREAM_I8_NB64 4
+#define DD_STREAM_I8_NB64 2
 #endif
 #ifndef DD_STREAM_I8_NW64
 #define DD_STREAM_I8_NW64 4
