@@ -16,8 +16,11 @@ Prints ONE JSON line (the driver's contract) with:
   cpu_baseline the PyTorch CPU restatement (page gather + masked GQA SDPA,
                fp32) timed on the whole batch with every core of the
                affinity mask (a few seconds per step)
-Extra decode configurations (--config c2f32 / c3 / c3g32 / c5 / c5f32) are available for study;
-the default line is C2.
+  other_configs  (a run without --config only) C3, C4 and C5 measured in the same run:
+               value, ms_per_step and roofline of each (their own lines via
+               --config)
+Extra configurations (--config c2f32 / c3 / c3g32 / c4 / c4f32 / c5 / c5f32 / rope / copy) print
+their own lines; the default line is C2.
 """
 import argparse
 import json
@@ -208,6 +211,8 @@ def main():
                     help='c4/c4f32: also time ragged_attention (decode rows overlapped on a side stream)')
     ap.add_argument('--config', default='c2', choices=['c2', 'c2f32', 'c3', 'c3g32', 'c4', 'c4f32', 'c5', 'c5f32', 'rope', 'copy'])
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--no-other-configs', action='store_true',
+                    help='c2: leave out the C3 / C4 / C5 summaries of the default line')
     ap.add_argument('--head-dim', type=int, default=128,
                     help='c4/c4f32: head size of the mixed batch (BASELINE C4 is 128)')
     ap.add_argument('--copy-probe', action='store_true',
@@ -226,18 +231,43 @@ def main():
               '(decode shards by sequence with no exchange; see the design notes)', file=sys.stderr)
         raise SystemExit(2)
 
-    from damendaemon_amd import kernels
     dev = 'cuda:0'
     torch.cuda.set_device(0)
     if args.config == 'c4':
-        return bench_mixed(args, dev)
-    if args.config == 'c4f32':
-        return bench_mixed(args, dev, torch.float32)
-    if args.config == 'rope':
-        return bench_rope(args, dev)
-    if args.config == 'copy':
-        return bench_copy(args, dev)
-    case, workload, dtype, nbytes = build_case(args.config, dev)
+        line = bench_mixed(args, dev)
+    elif args.config == 'c4f32':
+        line = bench_mixed(args, dev, torch.float32)
+    elif args.config == 'rope':
+        line = bench_rope(args, dev)
+    elif args.config == 'copy':
+        line = bench_copy(args, dev)
+    else:
+        line = bench_decode(args, dev, args.config)
+    explicit = any(a == '--config' or a.startswith('--config=') for a in sys.argv[1:])
+    if args.config == 'c2' and not explicit and not args.no_other_configs:
+        # The other BASELINE configurations, measured in the same run (no CPU
+        # baseline, 20 steps each), so that one default run records them all.
+        sub = argparse.Namespace(**{**vars(args), 'steps': 20, 'warmup': 3, 'no_cpu_baseline': True,
+                                    'ragged': False, 'head_dim': 128})
+        line['other_configs'] = {name: _summary(fn()) for name, fn in (
+            ('c3', lambda: bench_decode(sub, dev, 'c3')),
+            ('c4', lambda: bench_mixed(sub, dev)),
+            ('c5', lambda: bench_decode(sub, dev, 'c5')))}
+    print(json.dumps(line), flush=True)
+
+
+def _summary(line):
+    keep = ('split_kernel_ms', 'merge_kernel_ms', 'prefill_kernel_ms', 'decode_ms', 'step_hbm_gbps')
+    return {'workload': line['config']['workload'], 'value': line['value'], 'unit': line['unit'],
+            'ms_per_step': line['ms_per_step'], 'dtype': line['dtype'],
+            'roofline': {k: line['roofline'][k] for k in ('bound', 'achieved', 'peak', 'unit', 'frac', 'traffic')},
+            **{k: line['config'][k] for k in keep if line['config'].get(k) is not None}}
+
+
+def bench_decode(args, dev, config):
+    """One decode configuration (C2, C3, C5 and their variants): the line for it."""
+    from damendaemon_amd import kernels
+    case, workload, dtype, nbytes = build_case(config, dev)
     launch = kernels.prepare_attention(case['query'], case['cache_k'], case['cache_v'], case['positions'],
                                        case['slots'], page_table=case['page_table'],
                                        k_scale=case.get('k_scale'), v_scale=case.get('v_scale'))
@@ -307,11 +337,11 @@ def main():
                    'step_hbm_gbps': nbytes / (ms_per_step * 1e-3) / 1e9,
                    'graph_replay_ms_per_step': graph_ms},
         'roofline': {'bound': 'hbm', 'achieved': achieved, 'peak': PEAK_HBM_GBPS, 'unit': 'GB/s',
-                     'frac': achieved / PEAK_HBM_GBPS, 'traffic': measured_traffic(f'decode_{args.config}_pmc'),
+                     'frac': achieved / PEAK_HBM_GBPS, 'traffic': measured_traffic(f'decode_{config}_pmc'),
                      'algorithmic_bytes': nbytes, 'source_digest': source_digest('decode')},
         'cpu_baseline': None if args.no_cpu_baseline else cpu_baseline(case),
     }
-    print(json.dumps(line), flush=True)
+    return line
 
 
 def bench_mixed(args, dev, dtype=torch.bfloat16):
@@ -377,7 +407,7 @@ def bench_mixed(args, dev, dtype=torch.bfloat16):
     ctx = [s + n for s, n in zip(starts, lengths)]
     decode_bytes = sum(ctx[n_chunks:]) * 8 * D * 2 * (4 if f32 else 2)
     ms = wall / args.steps * 1e3
-    print(json.dumps({
+    return {
         'metric': 'mixed chunked-prefill + decode attention: packed tokens/s, prefill MFMA utilisation, 1 MI355X',
         'value': sum(lengths) / (ms * 1e-3), 'unit': 'tokens/s', 'n_gpus': 1, 'steps': args.steps,
         'warmup': args.warmup, 'ms_per_step': ms, 'higher_is_better': True, 'scaling': 'weak',
@@ -393,8 +423,7 @@ def bench_mixed(args, dev, dtype=torch.bfloat16):
         'roofline': {'bound': 'mfma', 'achieved': tflops, 'peak': peak, 'unit': 'TFLOP/s',
                      'frac': tflops / peak,
                      'traffic': measured_traffic('prefill_c4_pmc', 'prefill') if not f32 and D == 128 else None},
-        'cpu_baseline': None if args.no_cpu_baseline or not decode_rows else cpu_baseline_mixed(case, n_chunks)}),
-        flush=True)
+        'cpu_baseline': None if args.no_cpu_baseline or not decode_rows else cpu_baseline_mixed(case, n_chunks)}
 
 
 def _event_mean_ms(fn, steps, warmup):
@@ -467,7 +496,7 @@ def bench_rope(args, dev):
                      'H32/KH8/D128, rotary dim 128, page 16; 4 independent batches used in turn', 'rope',
                      {'bytes_per_token': per_token, 'rotated_sets': ROTATE})
     line['roofline']['traffic'] = measured_traffic('rope_c4_kernel_trace', 'rope')
-    print(json.dumps(line), flush=True)
+    return line
 
 
 def bench_copy(args, dev):
@@ -509,7 +538,7 @@ def bench_copy(args, dev):
                      {'restore_ms': restore_ms, 'rotated_sets': ROTATE,
                       'restore_hbm_gbps': nbytes / (restore_ms * 1e-3) / 1e9})
     line['roofline']['traffic'] = measured_traffic('copy_pages_kernel_trace', 'copy')
-    print(json.dumps(line), flush=True)
+    return line
 
 
 if __name__ == '__main__':
