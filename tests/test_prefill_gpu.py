@@ -201,9 +201,11 @@ def test_prefill_wide_head_sizes_pages_windows(dim, page, window, heads, kvh):
     check(out, exp)
 
 
-@pytest.mark.parametrize('dim', [96, 80])
-@pytest.mark.parametrize('page,window,heads,kvh', [(16, 0, 32, 8), (32, 70, 8, 1), (16, 300, 130, 1)])
+@pytest.mark.parametrize('dim', [96, 80, 64, 48])
+@pytest.mark.parametrize('page,window,heads,kvh', [(16, 0, 32, 8), (32, 70, 8, 1), (64, 200, 4, 2), (16, 300, 130, 1)])
 def test_prefill_other_head_sizes_pages_windows(dim, page, window, heads, kvh):
+    """The 128 layout at 96 and 80 dims, the 64 layout (128-key tiles) at 64 and 48: larger
+    pages, windows, and 130 query heads per KV head (one query row per work item)."""
     lengths = [1, 77, 200] if heads <= 32 else [1, 9, 40]
     starts = [5, 0, 1500] if heads <= 32 else [0, 17, 100]
     out, exp = run_segments(lengths, starts, heads, kvh, dim, torch.bfloat16, seed=dim + page + window,
