@@ -44,9 +44,9 @@ extern "C" int dd_decode_splits_for(int max_context, int batch_kv, int dim, int 
   const int n = dd_decode_splits(max_context, batch_kv, &st);
   if (n <= 0) return n;
   // Measured on 64 sequences of U[512, 8192] keys at D = 256, bf16: 4 KV
-  // heads 198 us with 1,024-key splits vs 215 us with 1,408; 8 KV heads 346
-  // vs 354 us (not capped by this rule); 16 x 32768 keys on 2 KV heads keeps
-  // its 2,048 (178 us vs 189 us with 1,024).
+  // heads 186 us with 1,024-key splits vs 195 us with 1,408; 8 KV heads
+  // (not capped by this rule) 342 us either way; 16 x 32768 keys on 2 KV
+  // heads keeps its 2,048 (174 us vs 183 us with 1,024).
   constexpr long kSlots = 2L * 256;   // resident workgroups of the D = 256 kernel
   if (dim == 256 && (kv_dtype == DD_BF16 || kv_dtype == DD_F16) && batch_kv >= 128 &&
       (long)batch_kv * n < 4 * kSlots && st > 1024) {

@@ -747,14 +747,14 @@ int dispatch_d(const DecodeParams &p0, int D, hipStream_t s, int phase) {
         switch (D) {
           case 64: return launch_stream_i8<QT, 64, 1, DD_STREAM_I8_NB64, DD_STREAM_I8_NW64>(p, s, phase);
           case 128: return launch_stream_i8<QT, 128, 1, DD_STREAM_I8_NB128, DD_STREAM_I8_NW128>(p, s, phase);
-          case 256: return launch_stream_i8<QT, 256, 1, DD_STREAM_NB256, DD_STREAM_NW256>(p, s, phase);
+          case 256: return launch_stream_i8<QT, 256, 1, DD_STREAM_I8_NB256, DD_STREAM_I8_NW256>(p, s, phase);
           default: break;
         }
       } else if (p.group == 32) {
         switch (D) {
           case 64: return launch_stream_i8<QT, 64, 2, DD_STREAM_I8_NB64, DD_STREAM_I8_NW64>(p, s, phase);
           case 128: return launch_stream_i8<QT, 128, 4, DD_STREAM_NB128G, DD_STREAM_I8_NW128>(p, s, phase);
-          case 256: return launch_stream_i8<QT, 256, 8, DD_STREAM_NB256, DD_STREAM_NW256>(p, s, phase);
+          case 256: return launch_stream_i8<QT, 256, 8, DD_STREAM_I8_NB256, DD_STREAM_I8_NW256>(p, s, phase);
           default: break;
         }
       }

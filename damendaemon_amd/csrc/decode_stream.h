@@ -100,8 +100,17 @@ typedef __attribute__((address_space(3))) void lds_void;
 #ifndef DD_STREAM_I8_NW64
 #define DD_STREAM_I8_NW64 4
 #endif
+// D = 256, 16-bit pages: 4 waves x 1 stage (C2 contexts, bf16: H16/KH8 341-342 us vs
+// 352-353 us with 2 x 2, H16/KH4 187 vs 190 us; C5 176.7 vs 178.5 us)
 #ifndef DD_STREAM_NB256
-#define DD_STREAM_NB256 2
+#define DD_STREAM_NB256 1
+#endif
+// int8 pages at D = 256 (two stages, as every int8 shape)
+#ifndef DD_STREAM_I8_NB256
+#define DD_STREAM_I8_NB256 2
+#endif
+#ifndef DD_STREAM_I8_NW256
+#define DD_STREAM_I8_NW256 2
 #endif
 
 // f(integral_constant<int, I>) for I = 0 .. N-1, unrolled at compile time.
@@ -119,7 +128,7 @@ DD_DEV void static_for(F &&f) {
 #define DD_STREAM_NW128 8
 #endif
 #ifndef DD_STREAM_NW256
-#define DD_STREAM_NW256 2
+#define DD_STREAM_NW256 4
 #endif
 
 // Word 3 of a raw buffer resource (no swizzle, dword data format).
