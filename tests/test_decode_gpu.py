@@ -286,6 +286,20 @@ def test_alibi_sinks_relative_bias_with_splits():
         check(run_case(case, **dev_kw), oracle_case(case, **kw), torch.float16)
 
 
+@pytest.mark.parametrize('dim,dtype', [(80, torch.bfloat16), (200, torch.float16), (40, torch.float32)])
+def test_other_head_sizes_bias_terms(dim, dtype):
+    """The general kernel at head sizes without a streamed kernel, with ALiBi, sinks, T5
+    bias and a window, over several splits and 16 query heads per KV head (MQA-like)."""
+    g = torch.Generator().manual_seed(dim)
+    case = paged_decode_case([2, 333, 1800, 4100], 16, 1, dim, dtype, seed=dim, nan_fill=True)
+    heads = 16
+    for kw in ({'alibi': -torch.rand(heads, generator=g) * 0.02, 'sinks': torch.randn(heads, generator=g)},
+               {'relative_bias': torch.randn(heads, 32, generator=g), 'relative_max_distance': 128},
+               {'alibi': -torch.rand(heads, generator=g) * 0.02, 'window': 250}):
+        dev_kw = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in kw.items()}
+        check(run_case(case, **dev_kw), oracle_case(case, **kw), dtype)
+
+
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize('window', [0, 200])
 def test_dim96_streamed_padded_rows(dtype, window):
