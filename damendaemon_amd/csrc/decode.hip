@@ -48,6 +48,19 @@ extern "C" int dd_decode_splits_for(int max_context, int batch_kv, int dim, int 
   // (not capped by this rule) 342 us either way; 16 x 32768 keys on 2 KV
   // heads keeps its 2,048 (174 us vs 183 us with 1,024).
   constexpr long kSlots = 2L * 256;   // resident workgroups of the D = 256 kernel
+  // int8 pages carry about half the bytes per key, so a split of the same
+  // keys is half the work: about a third of the context per split, at most
+  // 2,752 keys, while the launch keeps DD_DECODE_MIN_WG workgroups (C3:
+  // 2,752-key splits 0.646-0.651 of 8 TB/s vs 0.635-0.637 with 1,408; the
+  // reference's group-32 scales 0.587 vs 0.574).
+  if (kv_dtype == DD_I8) {
+    long st8 = dd_cdiv(dd_cdiv(max_context, 3), 64) * 64;
+    if (st8 > 2752) st8 = 2752;
+    if (st8 > st && (long)batch_kv * dd_cdiv(max_context, st8) >= DD_DECODE_MIN_WG) {
+      if (split_tokens) *split_tokens = (int)st8;
+      return (int)dd_cdiv(max_context, st8);
+    }
+  }
   if (dim == 256 && (kv_dtype == DD_BF16 || kv_dtype == DD_F16) && batch_kv >= 128 &&
       (long)batch_kv * n < 4 * kSlots && st > 1024) {
     if (split_tokens) *split_tokens = 1024;

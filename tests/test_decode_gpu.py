@@ -393,7 +393,7 @@ def test_many_sequences_launch_order(batch, window, kind):
     sequences per wave) and past its 256-sequence limit, with contexts that
     end exactly on a split boundary, inside the first split and past it."""
     g = torch.Generator().manual_seed(batch + window)
-    split_tokens = kernels._splits(3072, batch * 2, 64, torch.bfloat16)[1]
+    split_tokens = kernels._splits(3072, batch * 2, 64, torch.int8 if kind == 'int8' else torch.bfloat16)[1]
     fixed = [1, split_tokens, 2 * split_tokens, split_tokens + 1, 3072]
     contexts = fixed + torch.randint(1, 3073, (batch - len(fixed),), generator=g).tolist()
     case = paged_decode_case(contexts, 8, 2, 64, torch.float32 if kind == 'int8' else torch.bfloat16,

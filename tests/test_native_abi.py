@@ -70,10 +70,16 @@ def test_split_policy_for_head_size():
     assert policy(8192, 512, 256, _native.BF16) == (6, 1408)     # 8 KV heads: six splits each, enough units
     assert policy(32768, 32, 256, _native.BF16) == (16, 2048)    # C5
     assert policy(8192, 512, 128, _native.BF16) == (6, 1408)     # C2
+    assert policy(8192, 512, 128, _native.I8) == (3, 2752)       # C3: longer int8 splits
+    assert policy(32768, 32, 256, _native.I8) == (16, 2048)      # the 512-workgroup floor wins
     for ctx in (300, 1000, 4096, 8192, 32768):
         for bkh in (1, 8, 100, 128, 300, 512, 4096):
-            for dim, dtype in ((64, _native.BF16), (128, _native.F32), (256, _native.F32), (256, _native.I8)):
+            for dim, dtype in ((64, _native.BF16), (128, _native.F32), (256, _native.F32)):
                 assert policy(ctx, bkh, dim, dtype) == plain(ctx, bkh)
+            splits, st = policy(ctx, bkh, 128, _native.I8)
+            assert st % 64 == 0 and plain(ctx, bkh)[1] <= st <= max(2752, plain(ctx, bkh)[1])
+            assert splits * st >= ctx > (splits - 1) * st
+            assert st == plain(ctx, bkh)[1] or bkh * splits >= 512
             splits, st = policy(ctx, bkh, 256, _native.BF16)
             assert st % 64 == 0 and 256 <= st <= plain(ctx, bkh)[1]
             assert splits * st >= ctx > (splits - 1) * st
