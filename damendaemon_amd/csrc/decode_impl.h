@@ -708,7 +708,7 @@ namespace dd_decode {
 #endif
 
 // Instantiated once per dtype pair in decode_<dtype>.hip.  bf16 / f16 / fp32
-// pages at D = 64, 96, 128, 256 and int8 pages with one scale per row or per
+// pages at D = 64, 96, 128, 256 (bf16 / f16 also 160, 192, 224) and int8 pages with one scale per row or per
 // 32 channels at D = 64, 128, 256 take the streamed kernels (decode_stream.h),
 // any number of query heads per KV head; int8 at D = 96, other int8
 // groupings and every other head size up to 256 that is a multiple of 8 (16
@@ -725,6 +725,9 @@ int dispatch_d(const DecodeParams &p0, int D, hipStream_t s, int phase) {
         case 64: return launch_stream<KVT, 64, DD_STREAM_NB64, DD_STREAM_NW64>(p, s, phase);
         case 96: return launch_stream<KVT, 96, DD_STREAM_NB96, DD_STREAM_NW96>(p, s, phase);
         case 128: return launch_stream<KVT, 128, DD_STREAM_NB128, DD_STREAM_NW128>(p, s, phase);
+        case 160: return launch_stream<KVT, 160, DD_STREAM_NB_MID, DD_STREAM_NW_MID>(p, s, phase);
+        case 192: return launch_stream<KVT, 192, DD_STREAM_NB_MID, DD_STREAM_NW_MID>(p, s, phase);
+        case 224: return launch_stream<KVT, 224, DD_STREAM_NB_MID, DD_STREAM_NW_MID>(p, s, phase);
         case 256: return launch_stream<KVT, 256, DD_STREAM_NB256, DD_STREAM_NW256>(p, s, phase);
         default: break;
       }

@@ -130,6 +130,15 @@ DD_DEV void static_for(F &&f) {
 #ifndef DD_STREAM_NW256
 #define DD_STREAM_NW256 4
 #endif
+// D = 160, 192, 224 (16-bit pages; rows padded like D = 96): 4 waves x 1 stage
+// (C2 contexts, H16/KH8: 0.73-0.76 of 8 TB/s; 8 x 1 0.69-0.72; the general
+// kernel 0.51-0.58)
+#ifndef DD_STREAM_NB_MID
+#define DD_STREAM_NB_MID 1
+#endif
+#ifndef DD_STREAM_NW_MID
+#define DD_STREAM_NW_MID 4
+#endif
 
 // Word 3 of a raw buffer resource (no swizzle, dword data format).
 constexpr int kRawBufferWord3 = 0x00020000;
