@@ -708,7 +708,7 @@ namespace dd_decode {
 #endif
 
 // Instantiated once per dtype pair in decode_<dtype>.hip.  bf16 / f16 / fp32
-// pages at D = 64, 96, 128, 256 (bf16 / f16 also 160, 192, 224) and int8 pages with one scale per row or per
+// pages at D = 64, 96, 128, 160, 192, 224, 256 and int8 pages with one scale per row or per
 // 32 channels at D = 64, 128, 256 take the streamed kernels (decode_stream.h),
 // any number of query heads per KV head; int8 at D = 96, other int8
 // groupings and every other head size up to 256 that is a multiple of 8 (16
@@ -739,6 +739,9 @@ int dispatch_d(const DecodeParams &p0, int D, hipStream_t s, int phase) {
         case 64: return launch_stream<DD_F32, 64, DD_STREAM_NB_F32, DD_STREAM_NW_F32>(p, s, phase);
         case 96: return launch_stream<DD_F32, 96, DD_STREAM_NB_F32, DD_STREAM_NW_F32_96>(p, s, phase);
         case 128: return launch_stream<DD_F32, 128, DD_STREAM_NB_F32, DD_STREAM_NW_F32>(p, s, phase);
+        case 160: return launch_stream<DD_F32, 160, DD_STREAM_NB_F32_256, DD_STREAM_NW_F32_256>(p, s, phase);
+        case 192: return launch_stream<DD_F32, 192, DD_STREAM_NB_F32_256, DD_STREAM_NW_F32_256>(p, s, phase);
+        case 224: return launch_stream<DD_F32, 224, DD_STREAM_NB_F32_256, DD_STREAM_NW_F32_256>(p, s, phase);
         case 256: return launch_stream<DD_F32, 256, DD_STREAM_NB_F32_256, DD_STREAM_NW_F32_256>(p, s, phase);
         default: break;
       }
