@@ -228,7 +228,7 @@ def test_int8_nan_scales_and_expired_rows(dim, group, window):
 @pytest.mark.parametrize('dim', [8, 16, 24, 32, 40, 48, 72, 80, 112, 144, 160, 192, 200, 224, 240])
 def test_other_head_sizes(dtype, dim):
     """Head sizes (multiples of 8) beyond the streamed kernels' 64/96/128/256: 160, 192 and
-    224 on the streamed kernel with padded LDS rows (16-bit pages), the rest on the general
+    224 on the streamed kernel with padded LDS rows, the rest on the general
     kernel's smallest layout that holds them, rows of the real length; NaN-filled pools,
     several splits, 4 query heads per KV head, with and without a window."""
     contexts = [1, 17, 300, 2100]
