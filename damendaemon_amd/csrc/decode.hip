@@ -43,11 +43,6 @@ extern "C" int dd_decode_splits_for(int max_context, int batch_kv, int dim, int 
   int st = 0;
   const int n = dd_decode_splits(max_context, batch_kv, &st);
   if (n <= 0) return n;
-  // Measured on 64 sequences of U[512, 8192] keys at D = 256, bf16: 4 KV
-  // heads 186 us with 1,024-key splits vs 195 us with 1,408; 8 KV heads
-  // (not capped by this rule) 342 us either way; 16 x 32768 keys on 2 KV
-  // heads keeps its 2,048 (174 us vs 183 us with 1,024).
-  constexpr long kSlots = 2L * 256;   // resident workgroups of the D = 256 kernel
   // int8 pages carry about half the bytes per key, so a split of the same
   // keys is half the work: about a third of the context per split, at most
   // 2,752 keys, while the launch keeps DD_DECODE_MIN_WG workgroups (C3:
@@ -61,10 +56,19 @@ extern "C" int dd_decode_splits_for(int max_context, int batch_kv, int dim, int 
       return (int)dd_cdiv(max_context, st8);
     }
   }
-  if (dim == 256 && (kv_dtype == DD_BF16 || kv_dtype == DD_F16) && batch_kv >= 128 &&
-      (long)batch_kv * n < 4 * kSlots && st > 1024) {
-    if (split_tokens) *split_tokens = 1024;
-    return (int)dd_cdiv(max_context, 1024);
+  // Head sizes 160-256 on 16-bit pages, many (sequence, KV head) pairs and
+  // few splits per resident workgroup: a longer split is a long unit of work
+  // for those kernels and too few of them leave CUs idle at the end, so
+  // splits of at most 768 keys.  Measured on 64 sequences of U[512, 8192]
+  // keys, bf16, 4 KV heads, with 768 / 1,024 / 1,408-key splits: D 256 182 /
+  // 186 / 195 us, D 224 175 / 180 / 186 us, D 160 125 / 127 / 131 us.  8 KV
+  // heads (not capped by this rule): 342 us either way at D 256; 16 x 32768
+  // keys on 2 KV heads keeps its 2,048 (174 us vs 183 us with 1,024).
+  constexpr long kSlots = 2L * 256;   // about two resident workgroups per CU
+  if (dim >= 160 && (kv_dtype == DD_BF16 || kv_dtype == DD_F16) && batch_kv >= 128 &&
+      (long)batch_kv * n < 4 * kSlots && st > 768) {
+    if (split_tokens) *split_tokens = 768;
+    return (int)dd_cdiv(max_context, 768);
   }
   if (split_tokens) *split_tokens = st;
   return n;

@@ -59,11 +59,11 @@ int dd_decode_splits(int max_context, int batch_kv, int *split_tokens);
  * The same policy for a given head size and page dtype (no counterpart in
  * the reference, whose split choice ignores both): dd_decode_splits, except
  * that int8 pages take longer splits (about a third of the context, at most
- * 2,752 keys, while the launch keeps 512 workgroups), and that at head size
- * 256 with 16-bit pages, at least 128 (sequence, KV head) pairs and fewer
- * than four splits per resident workgroup (2 per CU), splits hold at most
- * 1,024 keys (a longer split is a long unit of work for that kernel, and too
- * few of them leave CUs idle at the end).
+ * 2,752 keys, while the launch keeps 512 workgroups), and that at head sizes
+ * 160-256 with 16-bit pages, at least 128 (sequence, KV head) pairs and
+ * fewer than four splits per resident workgroup (2 per CU), splits hold at
+ * most 768 keys (a longer split is a long unit of work for those kernels,
+ * and too few of them leave CUs idle at the end).
  * Same return values.
  */
 int dd_decode_splits_for(int max_context, int batch_kv, int dim, int kv_dtype, int *split_tokens);

@@ -25,7 +25,7 @@ int main(void) {
   const int splits = dd_decode_splits(8192, 512, &tokens);
   CHECK(splits >= 1 && tokens % 64 == 0 && splits * tokens >= 8192);
   CHECK(dd_decode_splits(0, 1, &tokens) < 0);
-  CHECK(dd_decode_splits_for(8192, 256, 256, DD_BF16, &tokens) == 8 && tokens == 1024);
+  CHECK(dd_decode_splits_for(8192, 256, 256, DD_BF16, &tokens) == 11 && tokens == 768);
 
   int cols = 0, kt = 0;
   CHECK(dd_prefill_geometry(128, &cols, &kt) == DD_OK && cols > 0 && kt > 0);

@@ -49,9 +49,10 @@ def test_split_policy_covers_context():
 
 
 def test_split_policy_for_head_size():
-    """The head-size-aware policy equals the plain one except at head size 256
-    with 16-bit pages, many (sequence, KV head) pairs and few splits per
-    resident workgroup, where splits hold at most 1,024 keys."""
+    """The head-size-aware policy equals the plain one except for int8 pages
+    (longer splits) and at head sizes 160-256 with 16-bit pages, many
+    (sequence, KV head) pairs and few splits per resident workgroup, where
+    splits hold at most 768 keys."""
     from damendaemon_amd import _native
     lib = _native.library()
 
@@ -65,8 +66,9 @@ def test_split_policy_for_head_size():
         splits = lib.dd_decode_splits(ctx, bkh, ctypes.byref(tokens))
         return splits, tokens.value
 
-    assert policy(8192, 256, 256, _native.BF16) == (8, 1024)     # 64 sequences x 4 KV heads
-    assert policy(8192, 256, 256, _native.F16) == (8, 1024)
+    assert policy(8192, 256, 256, _native.BF16) == (11, 768)     # 64 sequences x 4 KV heads
+    assert policy(8192, 256, 160, _native.F16) == (11, 768)
+    assert policy(8192, 256, 128, _native.BF16) == plain(8192, 256)
     assert policy(8192, 512, 256, _native.BF16) == (6, 1408)     # 8 KV heads: six splits each, enough units
     assert policy(32768, 32, 256, _native.BF16) == (16, 2048)    # C5
     assert policy(8192, 512, 128, _native.BF16) == (6, 1408)     # C2
@@ -80,7 +82,7 @@ def test_split_policy_for_head_size():
             assert st % 64 == 0 and plain(ctx, bkh)[1] <= st <= max(2752, plain(ctx, bkh)[1])
             assert splits * st >= ctx > (splits - 1) * st
             assert st == plain(ctx, bkh)[1] or bkh * splits >= 512
-            splits, st = policy(ctx, bkh, 256, _native.BF16)
+            splits, st = policy(ctx, bkh, 224, _native.BF16)
             assert st % 64 == 0 and 256 <= st <= plain(ctx, bkh)[1]
             assert splits * st >= ctx > (splits - 1) * st
     assert lib.dd_decode_splits_for(0, 1, 256, _native.BF16, None) < 0
