@@ -708,11 +708,20 @@ namespace dd_decode {
 #endif
 
 // Instantiated once per dtype pair in decode_<dtype>.hip.  bf16 / f16 / fp32
-// pages at D = 64, 96, 128, 160, 192, 224, 256 and int8 pages with one scale per row or per
-// 32 channels at D = 64, 128, 256 take the streamed kernels (decode_stream.h),
-// any number of query heads per KV head; int8 at D = 96, other int8
-// groupings and every other head size up to 256 that is a multiple of 8 (16
-// for int8 pages) take decode_kernel.
+// pages at every head size up to 256 that is a multiple of 8 (in the
+// smallest streamed layout that holds it) and int8 pages with one scale per
+// row or per 32 channels at D = 64, 128, 256 take the streamed kernels
+// (decode_stream.h), any number of query heads per KV head; int8 pages at
+// the other head sizes (multiples of 16 up to 256) and other int8 groupings
+// take decode_kernel.
+// LDS layout of the streamed 16-bit / fp32 kernels for head size D: the
+// smallest of 64, 96, 128, 160, 192, 224, 256 that holds it (D a multiple of
+// 8; the layout's extra dims are zeros), or 0.
+inline int stream_layout(int D) {
+  if (D <= 0 || D % 8 || D > 256) return 0;
+  return D <= 64 ? 64 : (D + 31) / 32 * 32;
+}
+
 template <int KVT, int QT>
 int dispatch_d(const DecodeParams &p0, int D, hipStream_t s, int phase) {
   // streamed kernels: more than 16 query heads per KV head run as gsub
@@ -721,7 +730,7 @@ int dispatch_d(const DecodeParams &p0, int D, hipStream_t s, int phase) {
   p.gsub = (p.G + 15) / 16;
   if constexpr (DD_DECODE_STREAM && KVT == QT && (KVT == DD_BF16 || KVT == DD_F16)) {
     {
-      switch (D) {
+      switch (stream_layout(D)) {
         case 64: return launch_stream<KVT, 64, DD_STREAM_NB64, DD_STREAM_NW64>(p, s, phase);
         case 96: return launch_stream<KVT, 96, DD_STREAM_NB96, DD_STREAM_NW96>(p, s, phase);
         case 128: return launch_stream<KVT, 128, DD_STREAM_NB128, DD_STREAM_NW128>(p, s, phase);
@@ -735,7 +744,7 @@ int dispatch_d(const DecodeParams &p0, int D, hipStream_t s, int phase) {
   }
   if constexpr (DD_DECODE_STREAM && KVT == DD_F32 && QT == DD_F32) {
     {
-      switch (D) {
+      switch (stream_layout(D)) {
         case 64: return launch_stream<DD_F32, 64, DD_STREAM_NB_F32, DD_STREAM_NW_F32>(p, s, phase);
         case 96: return launch_stream<DD_F32, 96, DD_STREAM_NB_F32, DD_STREAM_NW_F32_96>(p, s, phase);
         case 128: return launch_stream<DD_F32, 128, DD_STREAM_NB_F32, DD_STREAM_NW_F32>(p, s, phase);

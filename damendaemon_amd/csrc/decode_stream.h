@@ -293,9 +293,10 @@ DD_DEV void stream_epilogue(const DecodeParams &p, float (*s_ml)[2][16], float *
   }
   __syncthreads();
 
-  for (int idx = threadIdx.x; idx < G * D; idx += 64 * NW) {
-    const int h = idx / D;
-    const int d = idx - h * D;
+  const int DR = p.DR;   // the head size (<= D): row stride of the output and partials
+  for (int idx = threadIdx.x; idx < G * DR; idx += 64 * NW) {
+    const int h = idx / DR;
+    const int d = idx - h * DR;
     float m2 = s_ml[0][0][h];
     for (int ww = 1; ww < NW; ++ww) m2 = fmaxf(m2, s_ml[ww][0][h]);
     float l = 0.f, acc = 0.f;
@@ -313,9 +314,9 @@ DD_DEV void stream_epilogue(const DecodeParams &p, float (*s_ml)[2][16], float *
         l = l * f + fast_exp2(sk - m3);
         acc *= f;
       }
-      store_as<DT>(p.out, bh * D + d, acc / l);
+      store_as<DT>(p.out, bh * DR + d, acc / l);
     } else {
-      p.part[(bh * p.splits + split) * D + d] = acc / l;
+      p.part[(bh * p.splits + split) * DR + d] = acc / l;
       if (d == 0) p.lse[bh * p.splits + split] = m2 + log2f(l);
     }
   }
@@ -385,17 +386,24 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
 
   // Q^T operand: lane (head n16, dims 8kg + 32c ..+8); fp32: dims
   // (D/4) kg + 4c ..+4, one v_mfma_f32_16x16x4_f32 per dim of the four.
+  // The head size DR may be below the layout's D (by 16, for head sizes that
+  // are odd multiples of 16): rows are DR elements long in memory, and the
+  // dims DR .. D-1 are zero queries, zero K/V in LDS and never stored.
+  const int DR = p.DR;
+  const int ROWG = (F32 ? 4 : 2) * DR;   // bytes per token row in memory
   u32x4 qa[NC];
   if constexpr (F32) {
     const float *qf = (const float *)p.q;
 #pragma unroll
     for (int c = 0; c < NC; ++c)
-      qa[c] = col_on ? *(const u32x4 *)(qf + (head0 + n16) * D + (D / 4) * kg + 4 * c) : u32x4{0, 0, 0, 0};
+      qa[c] = col_on && (D / 4) * kg + 4 * c < DR ? *(const u32x4 *)(qf + (head0 + n16) * DR + (D / 4) * kg + 4 * c)
+                                                  : u32x4{0, 0, 0, 0};
   } else {
     const unsigned short *qb = (const unsigned short *)p.q;
 #pragma unroll
     for (int c = 0; c < NC; ++c)
-      qa[c] = col_on ? *(const u32x4 *)(qb + (head0 + n16) * D + 8 * kg + 32 * c) : u32x4{0, 0, 0, 0};
+      qa[c] = col_on && 8 * kg + 32 * c < DR ? *(const u32x4 *)(qb + (head0 + n16) * DR + 8 * kg + 32 * c)
+                                             : u32x4{0, 0, 0, 0};
   }
   float slope = (p.alibi && col_on) ? p.alibi[(long)kh * p.G + gofs + n16] * kLog2e : 0.f;
 
@@ -407,10 +415,10 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
     const int e = 64 * j + lane;
     if constexpr (PADR) {
       const int r = e / SPR, c = e % SPR;
-      dma_off[j] = r < 16 && c < CPR ? (unsigned)(r * ROWB + 16 * c) : 0x40000000u;
+      dma_off[j] = r < 16 && 16 * c < ROWG ? (unsigned)(r * ROWG + 16 * c) : 0x40000000u;
     } else {
-      const int r = e / CPR;
-      dma_off[j] = (unsigned)(r * ROWB + 16 * ((e % CPR) ^ stream_swz_of<DT, D>(r)));
+      const int r = e / CPR, c = (e % CPR) ^ stream_swz_of<DT, D>(r);
+      dma_off[j] = 16 * c < ROWG ? (unsigned)(r * ROWG + 16 * c) : 0x40000000u;
     }
   }
   unsigned k_addr[NC];
@@ -473,15 +481,15 @@ __global__ __launch_bounds__(64 * NW) void stream_kernel(DecodeParams p) {
         const int entry = pg >> p.chunk_shift;
         const long phys = tab[(long)row * p.table_w + entry];
         if (phys >= 0 && phys < p.capacity)
-          base = ((phys * p.KH + kh) * (long)p.page + ((pg - (entry << p.chunk_shift)) << 4)) * (long)D;
+          base = ((phys * p.KH + kh) * (long)p.page + ((pg - (entry << p.chunk_shift)) << 4)) * (long)DR;
       }
     } else {
-      base = (row >= 0 && row < p.capacity) ? (((long)row * p.KH + kh) * (long)p.page + (long)pg * 16) * (long)D : -1;
+      base = (row >= 0 && row < p.capacity) ? (((long)row * p.KH + kh) * (long)p.page + (long)pg * 16) * (long)DR : -1;
     }
     base = (long)uniform_ptr((const char *)base);
     const int live = base < 0 ? 0 : max(0, min(16, s_hi - pg * 16));
     const long off = base < 0 ? 0 : (F32 ? 4 : 2) * base;
-    const int bytes = uniform(live * ROWB);
+    const int bytes = uniform(live * ROWG);
     return ChunkRsrc{
         __builtin_amdgcn_make_buffer_rsrc((void *)uniform_ptr(kplane + off), (short)0, bytes, kRawBufferWord3),
         __builtin_amdgcn_make_buffer_rsrc((void *)uniform_ptr(vplane + off), (short)0, bytes, kRawBufferWord3)};
@@ -693,8 +701,8 @@ int launch_stream(const DecodeParams &p, hipStream_t stream, int phase) {
     DD_LAUNCH_CHECK();
   }
   if ((phase & 2) && p.splits > 1) {
-    hipLaunchKernelGGL((merge_kernel<DT>), dim3((unsigned)((long)p.B * p.H)), dim3(D < 256 ? D : 256), 0, stream,
-                       p, D);
+    hipLaunchKernelGGL((merge_kernel<DT>), dim3((unsigned)((long)p.B * p.H)), dim3(p.DR < 256 ? p.DR : 256), 0,
+                       stream, p, p.DR);
     DD_LAUNCH_CHECK();
   }
   return DD_OK;
@@ -1191,8 +1199,8 @@ int launch_stream_i8(const DecodeParams &p_in, hipStream_t stream, int phase) {
     DD_LAUNCH_CHECK();
   }
   if ((phase & 2) && p.splits > 1) {
-    hipLaunchKernelGGL((merge_kernel<QT>), dim3((unsigned)((long)p.B * p.H)), dim3(D < 256 ? D : 256), 0, stream,
-                       p, D);
+    hipLaunchKernelGGL((merge_kernel<QT>), dim3((unsigned)((long)p.B * p.H)), dim3(p.DR < 256 ? p.DR : 256), 0,
+                       stream, p, p.DR);
     DD_LAUNCH_CHECK();
   }
   return DD_OK;

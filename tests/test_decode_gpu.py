@@ -227,10 +227,10 @@ def test_int8_nan_scales_and_expired_rows(dim, group, window):
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize('dim', [8, 16, 24, 32, 40, 48, 72, 80, 112, 144, 160, 192, 200, 224, 240])
 def test_other_head_sizes(dtype, dim):
-    """Head sizes (multiples of 8) beyond the streamed kernels' 64/96/128/256: 160, 192 and
-    224 on the streamed kernel with padded LDS rows, the rest on the general
-    kernel's smallest layout that holds them, rows of the real length; NaN-filled pools,
-    several splits, 4 query heads per KV head, with and without a window."""
+    """Head sizes (multiples of 8) other than 64/96/128/256: 16-bit and fp32 pages on the
+    streamed kernel in the smallest of its 64/96/128/160/192/224/256 layouts that holds
+    them (the extra dims zeros), rows of the real length; NaN-filled pools, several
+    splits, 4 query heads per KV head, with and without a window."""
     contexts = [1, 17, 300, 2100]
     case = paged_decode_case(contexts, 12, 3, dim, dtype, seed=dim, nan_fill=True)
     check(run_case(case), oracle_case(case), dtype)
@@ -290,9 +290,8 @@ def test_alibi_sinks_relative_bias_with_splits():
 @pytest.mark.parametrize('dim,dtype', [(80, torch.bfloat16), (200, torch.float16), (40, torch.float32), (160, torch.bfloat16),
                                        (192, torch.float16), (224, torch.bfloat16)])
 def test_other_head_sizes_bias_terms(dim, dtype):
-    """Head sizes outside 64/96/128/256 (the general kernel; 160/192/224 the streamed one)
-    with ALiBi, sinks, T5 bias and a window, over several splits and 16 query heads per KV
-    head (MQA-like)."""
+    """Head sizes outside 64/96/128/256 with ALiBi, sinks, T5 bias and a window, over
+    several splits and 16 query heads per KV head (MQA-like)."""
     g = torch.Generator().manual_seed(dim)
     case = paged_decode_case([2, 333, 1800, 4100], 16, 1, dim, dtype, seed=dim, nan_fill=True)
     heads = 16
