@@ -302,6 +302,15 @@ def test_other_head_sizes_bias_terms(dim, dtype):
         check(run_case(case, **dev_kw), oracle_case(case, **kw), dtype)
 
 
+@pytest.mark.parametrize('dim,dtype', [(80, torch.bfloat16), (176, torch.float16), (48, torch.float32)])
+def test_other_head_sizes_wide_groups(dim, dtype):
+    """Head sizes below their streamed layout's with more than 16 query heads per KV head
+    (40 on one KV head: three workgroups of up to 16 heads over the same keys)."""
+    case = paged_decode_case([5, 700, 3000], 40, 1, dim, dtype, seed=dim + 40, nan_fill=True)
+    check(run_case(case), oracle_case(case), dtype)
+    check(run_case(case, window=100), oracle_case(case, window=100), dtype)
+
+
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize('window', [0, 200])
 def test_dim96_streamed_padded_rows(dtype, window):
