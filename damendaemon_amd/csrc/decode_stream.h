@@ -1,4 +1,9 @@
-// Streamed split-KV decode for bf16 / f16 KV pages (gfx950), D in {64,128,256}.
+// Streamed split-KV decode (gfx950) for bf16 / f16 / fp32 KV pages at every
+// head size up to 256 that is a multiple of 8 (LDS layouts of 64, 96, 128,
+// 160, 192, 224 and 256 dims; a smaller head size takes the smallest layout
+// that holds it, its rows of the real length in memory and the layout's
+// extra dims zeros), and for int8 pages at 64, 128 and 256 (stream_i8_kernel
+// below).
 //
 // Same contract as decode_kernel (the reference's `_attention`,
 // damendaemon/kernels.py:134-187): one query row per sequence, keys
@@ -8,9 +13,9 @@
 //
 // Memory path.  Each of the NW waves of a workgroup (sequence, KV head,
 // split) owns every NW-th 16-token chunk and a private ring of NB LDS
-// stages (bf16/f16 at D = 128 and fp32 at D = 64 / 128: 8 waves x 1 stage,
-// measured 1 % (16-bit) and 7 % (fp32) faster on 64 ragged contexts than
-// 4 waves x 2; fp32 at D = 96 and 256: 4 waves x 1 stage).  A chunk's K
+// stages (16-bit pages: 8 waves x 1 stage up to D = 128, 4 x 1 from 160;
+// fp32 at D = 64 / 128: 8 x 1, measured 1 % (16-bit) and 7 % (fp32) faster
+// on 64 ragged contexts than 4 waves x 2; fp32 at 96 and from 160: 4 x 1).  A chunk's K
 // and V rows are copied HBM -> LDS by direct-to-LDS buffer loads (no VGPRs
 // held while in flight), marked nontemporal because
 // every KV byte is read exactly once per step.  A stage is refilled as soon
