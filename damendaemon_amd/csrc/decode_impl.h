@@ -10,7 +10,11 @@
 //     denominator once (kernels.py:168-176, 198-206);
 //   * long contexts are split; splits are combined by log-sum-exp.
 //
-// MI355X design (not a translation of the Triton kernel):
+// The streamed kernels of decode_stream.h take every 16-bit and fp32 case and
+// int8 pages at head sizes 64, 128 and 256; decode_kernel below, the general
+// kernel, serves the remaining int8 cases.
+//
+// General kernel (not a translation of the Triton kernel):
 //   * one workgroup = one (sequence, KV head, split); its 4 wavefronts take
 //     interleaved 16-token pages, so every K/V byte is read once for the
 //     whole GQA group (the reference re-reads K/V per query head);
