@@ -10,8 +10,9 @@
 //     denominator once (kernels.py:168-176, 198-206);
 //   * long contexts are split; splits are combined by log-sum-exp.
 //
-// The streamed kernels of decode_stream.h take every 16-bit and fp32 case and
-// int8 pages at head sizes 64, 128 and 256; decode_kernel below, the general
+// The streamed kernels of decode_stream.h take every 16-bit and fp32 case,
+// int8 pages with one scale per row at every head size and int8 pages with
+// group-32 scales at 64, 128 and 256; decode_kernel below, the general
 // kernel, serves the remaining int8 cases.
 //
 // General kernel (not a translation of the Triton kernel):
@@ -713,11 +714,11 @@ namespace dd_decode {
 
 // Instantiated once per dtype pair in decode_<dtype>.hip.  bf16 / f16 / fp32
 // pages at every head size up to 256 that is a multiple of 8 (in the
-// smallest streamed layout that holds it) and int8 pages with one scale per
-// row or per 32 channels at D = 64, 128, 256 take the streamed kernels
-// (decode_stream.h), any number of query heads per KV head; int8 pages at
-// the other head sizes (multiples of 16 up to 256) and other int8 groupings
-// take decode_kernel.
+// smallest streamed layout that holds it), int8 pages with one scale per row
+// at every head size that is a multiple of 16 (the same way) and int8 pages
+// with group-32 scales at D = 64, 128, 256 take the streamed kernels
+// (decode_stream.h), any number of query heads per KV head; the other int8
+// groupings take decode_kernel.
 // LDS layout of the streamed 16-bit / fp32 kernels for head size D: the
 // smallest of 64, 96, 128, 160, 192, 224, 256 that holds it (D a multiple of
 // 8; the layout's extra dims are zeros), or 0.
@@ -762,8 +763,10 @@ int dispatch_d(const DecodeParams &p0, int D, hipStream_t s, int phase) {
   }
   if constexpr (DD_DECODE_STREAM && KVT == DD_I8 && (QT == DD_BF16 || QT == DD_F16)) {
     {
-      if (p.group == D) {
-        switch (D) {
+      if (p.group == D && D % 16 == 0) {
+        // one scale per row: the smallest of the 64 / 128 / 256 layouts
+        // that holds the head size (its extra dims zeros)
+        switch (D <= 64 ? 64 : D <= 128 ? 128 : D <= 256 ? 256 : 0) {
           case 64: return launch_stream_i8<QT, 64, 1, DD_STREAM_I8_NB64, DD_STREAM_I8_NW64>(p, s, phase);
           case 128: return launch_stream_i8<QT, 128, 1, DD_STREAM_I8_NB128, DD_STREAM_I8_NW128>(p, s, phase);
           case 256: return launch_stream_i8<QT, 256, 1, DD_STREAM_I8_NB256, DD_STREAM_I8_NW256>(p, s, phase);

@@ -2,8 +2,9 @@
 // head size up to 256 that is a multiple of 8 (LDS layouts of 64, 96, 128,
 // 160, 192, 224 and 256 dims; a smaller head size takes the smallest layout
 // that holds it, its rows of the real length in memory and the layout's
-// extra dims zeros), and for int8 pages at 64, 128 and 256 (stream_i8_kernel
-// below).
+// extra dims zeros), and for int8 pages (stream_i8_kernel below: one scale
+// per row at every head size that is a multiple of 16, in layouts of 64, 128
+// and 256 dims; group-32 scales at 64, 128 and 256).
 //
 // Same contract as decode_kernel (the reference's `_attention`,
 // damendaemon/kernels.py:134-187): one query row per sequence, keys
@@ -820,12 +821,17 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
   const long head0 = (long)b * p.H + (long)kh * p.G + gofs;
   const bool col_on = n16 < G;
 
+  // The head size DR may be below the layout's D (one scale per row only):
+  // rows are DR bytes in memory, the layout's dims DR .. D-1 are zero
+  // queries and zero bytes in LDS, and they are never stored.
+  const int DR = p.DR;
   u32x4 qa[NC];
   {
     const unsigned short *qb = (const unsigned short *)p.q;
 #pragma unroll
     for (int c = 0; c < NC; ++c)
-      qa[c] = col_on ? *(const u32x4 *)(qb + (head0 + n16) * D + 8 * kg + 32 * c) : u32x4{0, 0, 0, 0};
+      qa[c] = col_on && 8 * kg + 32 * c < DR ? *(const u32x4 *)(qb + (head0 + n16) * DR + 8 * kg + 32 * c)
+                                             : u32x4{0, 0, 0, 0};
   }
   float slope = (p.alibi && col_on) ? p.alibi[(long)kh * p.G + gofs + n16] * kLog2e : 0.f;
 
@@ -888,11 +894,11 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
       base = (long)uniform_ptr((const char *)base);
       const int live = base < 0 ? 0 : max(0, min(16, s_hi - pg * 16));
       const long rb = base < 0 ? 0 : base;  // token-row index
-      const int bytes = uniform(live * ROWB);
+      const int bytes = uniform(live * DR);
       const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-          (void *)uniform_ptr(kplane + rb * ROWB), (short)0, bytes, kRawBufferWord3);
+          (void *)uniform_ptr(kplane + rb * DR), (short)0, bytes, kRawBufferWord3);
       const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-          (void *)uniform_ptr(vplane + rb * ROWB), (short)0, bytes, kRawBufferWord3);
+          (void *)uniform_ptr(vplane + rb * DR), (short)0, bytes, kRawBufferWord3);
       const int sbytes = uniform(base < 0 ? 0 : SCB);
       const __amdgpu_buffer_rsrc_t rks = __builtin_amdgcn_make_buffer_rsrc(
           (void *)uniform_ptr(ksplane + rb * 2 * NG), (short)0, sbytes, kRawBufferWord3);
@@ -903,7 +909,7 @@ __global__ __launch_bounds__(64 * NW) void stream_i8_kernel(DecodeParams p) {
         const int e = 64 * j + lane;
         const int r = e / CPR16;
         const int src16 = (e % CPR16) ^ (i8_swz<D>(16 * ch + r) >> 1);
-        const unsigned off = (unsigned)(r * ROWB + 16 * src16);
+        const unsigned off = 16 * src16 < DR ? (unsigned)(r * DR + 16 * src16) : 0x40000000u;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void *)(dst + KOFF + ch * CHB + 1024 * j), 16, off, 0,
                                                  0, kStreamLoadAux);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void *)(dst + VOFF + ch * CHB + 1024 * j), 16, off, 0,
