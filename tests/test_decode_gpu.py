@@ -237,19 +237,20 @@ def test_other_head_sizes(dtype, dim):
     check(run_case(case, window=45), oracle_case(case, window=45), dtype)
 
 
-@pytest.mark.parametrize('dim,group', [(48, 48), (80, 80), (160, 160), (160, 32), (192, 32), (224, 224)])
-def test_int8_other_head_sizes(dim, group):
+@pytest.mark.parametrize('dim,group', [(48, 48), (80, 80), (96, 96), (160, 160), (160, 32), (192, 32), (224, 224)])
+@pytest.mark.parametrize('window', [0, 90])
+def test_int8_other_head_sizes(dim, group, window):
     """Q8 pages at head sizes without a streamed kernel, NaN scales on unused rows."""
     contexts = [1, 15, 17, 300, 1111]
     case = paged_decode_case(contexts, 12, 3, dim, torch.float32, seed=dim + group, nan_fill=True)
     qk, ks = oracle.quantize_q8(case['cache_k'], group)
     qv, vs = oracle.quantize_q8(case['cache_v'], group)
     expected = oracle.decode_attention(case['query'].to(torch.bfloat16), qk, qv, case['positions'], case['slots'],
-                                       page_table=case['page_table'], k_scale=ks, v_scale=vs)
+                                       page_table=case['page_table'], k_scale=ks, v_scale=vs, window=window)
     ks[~torch.isfinite(ks)] = float('nan')
     vs[~torch.isfinite(vs)] = float('nan')
     case.update(cache_k=qk, cache_v=qv, k_scale=ks, v_scale=vs, query=case['query'].to(torch.bfloat16))
-    check(run_case(case), expected, torch.int8)
+    check(run_case(case, window=window), expected, torch.int8)
 
 
 def test_unsupported_head_size_refused():

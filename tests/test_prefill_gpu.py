@@ -89,12 +89,13 @@ def test_prefill_running_max_moves(dtype, slope):
 
 
 @pytest.mark.parametrize('dim,dtype', [(128, torch.bfloat16), (256, torch.bfloat16), (96, torch.float16),
-                                       (64, torch.float16), (160, torch.bfloat16), (144, torch.float16)])
+                                       (64, torch.float16), (160, torch.bfloat16), (144, torch.float16),
+                                       (80, torch.bfloat16)])
 def test_mixed_batch_end_to_end(dim, dtype):
     """Config C4 at reduced size: pack on the GPU, write the new K/V into the pages, attend
-    (prefill chunks and decode rows on their two streams), at head sizes both the streamed
-    decode and the 16-bit prefill kernels take, and at 160 and 144 (the prefill kernel's 160
-    layout; the decode rows on the general decode kernel)."""
+    (prefill chunks and decode rows on their two streams), at head sizes 64-256 including
+    160 and 144 (the prefill kernel's 160 layout) and 80 (the prefill's 128 layout, the
+    decode's 96 layout)."""
     rng = random.Random(4 + dim)
     heads, kvh = 32, 8
     starts = [rng.randint(0, 1024) for _ in range(3)] + [rng.randint(256, 2048) - 1 for _ in range(20)]
